@@ -1,0 +1,227 @@
+"""Benchmark of the fp8 quantized-linear path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-extra]
+
+A step is one pass of the hot path over the DiT QKV projection: per-token e4m3
+quantization of X [32760, 5120] followed by the fp8 GEMM against the fused QKV weight
+[15360, 5120] with per-token x per-channel dequantization and the bias fused in. Inputs
+are synthetic (seeded), resident in HBM before the timed region. Prints ONE JSON line:
+
+  value       whole-step throughput, 2*M*N*K / step time (TFLOP/s)
+  roofline    the GEMM kernel alone, from HIP events on the stream it runs on, against
+              the dense fp8 MFMA peak (5.03 PFLOP/s)
+  cpu_baseline  the oracle (C row quantizer + numpy fp32 dequantized matmul) on a row
+              sample of the same workload, on this host's cores
+  extra       the quantizer's HBM rate, the weight requantizer (plain and with the fused
+              rank-64 LoRA merge), the other DiT GEMMs and the ms of one block's four
+              linears (QKV, attention-out + gate, FFN-up + GELU, FFN-down + gate)
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vdn-minimax-h3_amd"))
+
+METRIC = "fp8 linear TFLOP/s & % fp8 MFMA peak (M=32760 QKV); ms per DiT-block linears"
+PEAK_FP8_TFLOPS = 5030.0     # 256 CU x 2.4 GHz x 8192 FLOP/clk/CU, dense
+PEAK_HBM_GBPS = 8000.0
+
+
+def _events(n):
+    import torch
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _gpu_clock():
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20)
+        lines = [l.strip() for l in r.stdout.splitlines() if "sclk" in l.lower()]
+        return lines[0] if lines else None
+    except Exception:
+        return None
+
+
+def _time_region(fn, reps):
+    """Mean ms of fn() over reps launches, from HIP events on the current stream."""
+    import torch
+    ev = _events(2 * reps)
+    for i in range(reps):
+        ev[2 * i].record()
+        fn()
+        ev[2 * i + 1].record()
+    torch.cuda.synchronize()
+    return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
+
+
+def _make_linear(w, b, dev, lora=None):
+    import torch
+    import vdn_fp8
+    lin = torch.nn.Linear(w.shape[1], w.shape[0], bias=b is not None, dtype=torch.bfloat16, device="meta")
+    lin.weight = torch.nn.Parameter(w.to(dev), requires_grad=False)
+    lin.bias = torch.nn.Parameter(b.to(dev), requires_grad=False) if b is not None else None
+    return vdn_fp8.Fp8Linear(lin, lora=lora)
+
+
+def cpu_baseline(x, w, b, rows=2048, budget_s=12.0):
+    """The oracle on a row sample: quantize `rows` rows, fp32 dequantized matmul + bias.
+    Repeats over disjoint samples until `budget_s` of CPU time; returns TFLOP/s."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    cores = min(16, os.cpu_count() or 1)
+    os.environ["ORACLE_THREADS"] = str(cores)
+
+    def u16(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    wq, ws = O.quantize_weight(u16(w))                      # once, like Fp8Linear.__init__
+    wd = O.e4m3_decode(wq) * ws[:, None]
+    bias = O.bf16_decode(u16(b))
+    xb = u16(x)
+    done, spent, flops = 0, 0.0, 0.0
+    with threadpool_limits(limits=cores):
+        while spent < budget_s and done + rows <= xb.shape[0]:
+            t0 = time.perf_counter()
+            qx, sx = O.quantize_rows(xb[done:done + rows])
+            out = (O.e4m3_decode(qx) * sx[:, None]) @ wd.T + bias[None, :]
+            spent += time.perf_counter() - t0
+            flops += 2.0 * rows * w.shape[0] * w.shape[1]
+            done += rows
+            del out
+    return {"value": flops / spent / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{done} of {xb.shape[0]} rows of the QKV workload in {rows}-row batches: oracle C "
+                      f"row quantization + numpy fp32 dequantized matmul + bias ({spent:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the fp8 linear path has no cross-GPU step "
+              f"(rows shard without exchange); --gpus {args.gpus} is not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import vdn_fp8
+    from vdn_fp8 import workloads as wl
+
+    dev = torch.device("cuda:0")
+    x_cpu, w_cpu, b_cpu = wl.dit_qkv()
+    M, K = x_cpu.shape
+    N = w_cpu.shape[0]
+    x = x_cpu.to(dev)
+    lin = _make_linear(w_cpu, b_cpu, dev)
+
+    def step():
+        qx, sx = vdn_fp8.quantize_rows(x)
+        return lin.forward_quantized(qx, sx)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    ev = _events(3 * args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[3 * i].record()
+        qx, sx = vdn_fp8.quantize_rows(x)
+        ev[3 * i + 1].record()
+        lin.forward_quantized(qx, sx)
+        ev[3 * i + 2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    quant_ms = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(args.steps)) / args.steps
+    gemm_ms = sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(args.steps)) / args.steps
+    flops = wl.linear_flops(M, N, K)
+    gemm_tflops = flops / (gemm_ms * 1e-3) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("gemm_qkv")
+    line = {
+        "metric": METRIC, "value": round(flops / (ms_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) activations with 0.1% outlier channels x20, N(0,0.02) weights)",
+        "config": {"workload": "DiT QKV projection: quantize X + fp8 GEMM + bias", "M": M, "N": N, "K": K,
+                   "seed": 2, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_FP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
+                     "kernel": "k_gemm_fp8 (EPI none, bias)", "kernel_ms": round(gemm_ms, 4)},
+    }
+    extra = {"quantize_rows": {"ms": round(quant_ms, 4),
+                               "GB/s": round(wl.quant_bytes(M, K) / (quant_ms * 1e-3) / 1e9, 1)}}
+    extra["quantize_rows"]["frac_hbm"] = round(extra["quantize_rows"]["GB/s"] / PEAK_HBM_GBPS, 4)
+
+    if not args.no_extra:
+        reps = 10
+        # weight requantization, plain and with the fused rank-64 LoRA merge
+        w0, a, b, lscale, _ = wl.dit_lora(M=8)
+        w0d, ad, bd = w0.to(dev), a.to(dev), b.to(dev)
+        ms = _time_region(lambda: vdn_fp8.requantize_weight(w0d), reps)
+        extra["requantize_weight"] = {"shape": list(w0.shape), "ms": round(ms, 4),
+                                      "GB/s": round(wl.requant_bytes(*w0.shape) / (ms * 1e-3) / 1e9, 1)}
+        ms = _time_region(lambda: vdn_fp8.requantize_weight(w0d, lora=(ad, bd, lscale)), reps)
+        gbs = wl.requant_bytes(*w0.shape, rank=a.shape[0]) / (ms * 1e-3) / 1e9
+        extra["lora_merge_requantize"] = {"shape": list(w0.shape), "rank": a.shape[0], "ms": round(ms, 4),
+                                          "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
+        # one DiT block's four linears (QKV weight with the merged LoRA)
+        x_up, w_up, b_up = wl.dit_ffn_up(M=8)
+        (_, w_dn), (_, w_out), gate = wl.dit_ffn_down_attn_out(M=8)
+        qkv = _make_linear(w0, b_cpu, dev, lora=(ad, bd, lscale))
+        out_l = _make_linear(w_out, None, dev)
+        up_l = _make_linear(w_up, b_up, dev)
+        dn_l = _make_linear(w_dn, None, dev)
+        gate_d = gate.to(dev)
+        h = torch.empty(M, w_up.shape[0], dtype=torch.bfloat16, device=dev)
+
+        def block():
+            qx, sx = vdn_fp8.quantize_rows(x)
+            qkv.forward_quantized(qx, sx)
+            qx, sx = vdn_fp8.quantize_rows(x)
+            out_l.forward_quantized(qx, sx, epilogue="gate", gate=gate_d)
+            qx, sx = vdn_fp8.quantize_rows(x)
+            hh = up_l.forward_quantized(qx, sx, epilogue="gelu_tanh")
+            qh, sh = vdn_fp8.quantize_rows(hh)
+            dn_l.forward_quantized(qh, sh, epilogue="gate", gate=gate_d)
+
+        block()
+        extra["block_linears"] = {"ms": round(_time_region(block, reps), 4),
+                                  "flop": wl.linear_flops(M, 3 * 5120 + 5120 + 13824, 5120)
+                                  + wl.linear_flops(M, 5120, 13824)}
+        qx, sx = vdn_fp8.quantize_rows(x)
+        qh, sh = vdn_fp8.quantize_rows(h.normal_())
+        for name, fn, n_, k_ in (
+                ("gemm_attn_out_gate", lambda: out_l.forward_quantized(qx, sx, epilogue="gate", gate=gate_d), 5120, 5120),
+                ("gemm_ffn_up_gelu", lambda: up_l.forward_quantized(qx, sx, epilogue="gelu_tanh"), 13824, 5120),
+                ("gemm_ffn_down_gate", lambda: dn_l.forward_quantized(qh, sh, epilogue="gate", gate=gate_d), 5120, 13824)):
+            ms = _time_region(fn, reps)
+            tf = wl.linear_flops(M, n_, k_) / (ms * 1e-3) / 1e12
+            extra[name] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP8_TFLOPS, 4)}
+        ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
+        extra["quantize_rows_13824"] = {"ms": round(ms, 4),
+                                        "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
+        extra["gpu_clock"] = _gpu_clock()
+    line["extra"] = extra
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, b_cpu)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,129 @@
+/*
+ * vdn_fp8.h -- C ABI of the MI355X (gfx950) fp8 quantized-linear library,
+ * libvdnfp8.so.
+ *
+ * This is the drop-in boundary for the fp8 linear path of the VDN-H3 DiT
+ * blocks. The reference reaches the same arithmetic from Python through
+ * Triton kernels and torch._scaled_mm (src/models/ops/fp8_linear.py); each
+ * entry point below names the reference interface it replaces. The Python
+ * package vdn_fp8 binds these symbols with ctypes and keeps the reference's
+ * module API on top of them.
+ *
+ * Conventions
+ *   - Plain pointers to device memory (HBM) and sizes; no framework types.
+ *   - bf16 tensors are uint16 bit patterns; e4m3 tensors are OCP float8
+ *     e4m3 "fn" codes (torch.float8_e4m3fn: max 448, 0x7f/0xff NaN).
+ *   - Matrices are row-major with an explicit leading dimension in ELEMENTS.
+ *   - Every call is asynchronous on `stream` (NULL = the null stream) and
+ *     neither allocates nor frees device memory; the caller owns all buffers.
+ *   - Return 0 on success. A nonzero status leaves nothing launched, and
+ *     vdn_fp8_last_error() returns the message (per host thread). Calls are
+ *     re-entrant; the library keeps no mutable state besides that message.
+ *   - Scales: x_scale / w_scale are binary32, one per row of X / W.
+ */
+#ifndef VDN_FP8_H
+#define VDN_FP8_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VDN_FP8_ABI_VERSION 1
+
+/* status codes */
+#define VDN_FP8_OK 0
+#define VDN_FP8_EINVAL 1   /* a contract violation: shape, alignment, null */
+#define VDN_FP8_ELAUNCH 2  /* the HIP runtime refused the launch */
+
+/* GEMM epilogues, applied to v = bf16(bf16(x_scale[m] * w_scale[n] * acc[m][n]) + bias[n]) */
+#define VDN_FP8_EPI_NONE 0      /* out = v */
+#define VDN_FP8_EPI_GELU_TANH 1 /* out = 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) */
+#define VDN_FP8_EPI_GATE 2      /* out = gate[gate_index[m]][n] * v (+ residual[m][n]) */
+
+/*
+ * Per-token activation quantization: for each row m of x (bf16 [M, K]),
+ *   scale[m] = max(max_k |x[m][k]| / 448, 1e-12)        (binary32)
+ *   y[m][k]  = e4m3(x[m][k] / scale[m])                  (round to nearest even)
+ * bit-exact with the reference's eager spelling.
+ * Replaces: quantize_rows / _quantize_rows_kernel, src/models/ops/fp8_linear.py:110-117
+ *           and :66-80 (contract: quantize_rows_reference, :132-135).
+ * Requires: K % 8 == 0, ldx % 8 == 0, ldy % 8 == 0, x 16-byte and y 8-byte aligned.
+ */
+int vdn_fp8_quantize_rows(const void *x, int64_t M, int64_t K, int64_t ldx,
+                          void *y, int64_t ldy, float *scale, hipStream_t stream);
+
+/*
+ * Fused SwiGLU + per-token quantization of h (bf16 [M, 2K], value half first,
+ * gate half second): act = a * g * sigmoid(g) in binary32, never rounded to
+ * bf16, then the quantize_rows arithmetic on act (y e4m3 [M, K], scale [M]).
+ * Replaces: swiglu_quantize / _swiglu_quantize_kernel,
+ *           src/models/ops/fp8_linear.py:120-129 and :83-99.
+ * Requires: K % 8 == 0, ldh % 8 == 0, ldy % 8 == 0.
+ */
+int vdn_fp8_swiglu_quantize_rows(const void *h, int64_t M, int64_t K, int64_t ldh,
+                                 void *y, int64_t ldy, float *scale, hipStream_t stream);
+
+/*
+ * Rowwise weight quantization, optionally after a fused LoRA merge.
+ *   W' = W                                        if lora_a == NULL
+ *   W' = bf16(W + bf16(lora_scale * (B @ A)))     otherwise (fp32 accumulate)
+ *   w_scale[n] = max(max_k |W'[n][k]| / 448, 1e-12)          (binary32, stored)
+ *   wq[n][k]   = e4m3(bf16(W'[n][k] / bf16(w_scale[n])))     (two roundings)
+ * w bf16 [N, K] (row stride ldw); lora_a bf16 [rank, K] and lora_b bf16
+ * [N, rank], both contiguous; wq e4m3 [N, K] (row stride ldq). If w_merged is
+ * not NULL, W' is also written there (bf16 [N, K], row stride ldw; it may
+ * alias w -- the reference's in-place merge). With LoRA, wq and w_scale may
+ * both be NULL: the call is then the merge alone (merge_lora_state).
+ * Replaces: the rowwise branch of Fp8Linear.__init__,
+ *           src/models/ops/fp8_linear.py:262-267, preceded by the update of
+ *           merge_lora_state, src/inference/utils/lora.py:80-94.
+ * Requires: K % 8 == 0, ldw % 8 == 0, ldq % 8 == 0; with LoRA: 1 <= rank <= 128,
+ *           K % 16 == 0, lora_a 8-byte aligned, wq rows 4-byte aligned.
+ */
+int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
+                              const void *lora_a, const void *lora_b, int64_t rank,
+                              float lora_scale, void *wq, int64_t ldq, float *w_scale,
+                              void *w_merged, hipStream_t stream);
+
+/*
+ * fp8 x fp8 GEMM with per-token x per-output-channel dequantization and a
+ * fused epilogue:
+ *   acc[m][n] = sum_k xq[m][k] * wq[n][k]                 (fp32 accumulate)
+ *   v         = bf16(x_scale[m] * w_scale[n] * acc[m][n])
+ *   v         = bf16(v + bias[n])                          (bias optional)
+ *   out[m][n] = bf16(epilogue(v))                          (fp32 inside)
+ * The bf16 roundings sit where the reference's op sequence has them: the
+ * scaled GEMM's bf16 output, the bf16 bias add, the epilogue on that tensor.
+ * xq e4m3 [M, K] (row stride ldx), wq e4m3 [N, K] (row stride ldw) -- both
+ * K-contiguous, the layout of torch._scaled_mm(x_fp8, weight_fp8.t()).
+ * bias bf16 [N] or NULL. For VDN_FP8_EPI_GATE: gate bf16 [gate_rows, N] (row
+ * stride ldgate), gate_index int32 [M] (NULL = row 0 for every m; an index
+ * outside [0, gate_rows) is clamped into it), residual bf16 [M, N] (row stride
+ * ldres) or NULL. out bf16 [M, N] (row stride ldo).
+ * Replaces: Fp8Linear.forward_quantized, src/models/ops/fp8_linear.py:270-277
+ *           (torch._scaled_mm rowwise + bias add); the GELU epilogue has no
+ *           reference function; the gate epilogue replaces _post_ref /
+ *           the compiled `post`, src/models/ops/fused_block.py:47-49,101-110.
+ * Requires: K % 16 == 0; ldx, ldw % 16 == 0; ldo, ldres, ldgate % 4 == 0;
+ *           xq, wq 16-byte aligned; out, residual, gate, bias 8-byte aligned.
+ */
+int vdn_fp8_gemm(const void *xq, const float *x_scale, const void *wq, const float *w_scale,
+                 int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                 const void *bias, int epilogue, const void *gate, const int32_t *gate_index,
+                 int64_t gate_rows, int64_t ldgate, const void *residual, int64_t ldres,
+                 void *out, int64_t ldo, hipStream_t stream);
+
+/* The message of the last failed call on this host thread ("" if none). */
+const char *vdn_fp8_last_error(void);
+
+/* VDN_FP8_ABI_VERSION of the loaded library. */
+int vdn_fp8_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VDN_FP8_H */

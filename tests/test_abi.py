@@ -1,0 +1,90 @@
+"""The C-ABI library (no GPU needed): it loads, exports every symbol that
+include/vdn_fp8.h declares, reports its ABI version, and rejects contract
+violations with EINVAL before launching anything."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vdn_fp8.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(vdn_fp8_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_symbols()
+    assert {"vdn_fp8_quantize_rows", "vdn_fp8_swiglu_quantize_rows", "vdn_fp8_requantize_weight",
+            "vdn_fp8_gemm", "vdn_fp8_last_error", "vdn_fp8_abi_version"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    import vdn_fp8._lib as L
+    lib = L.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    bound = {n for n, _, _ in L.EXPORTS}
+    assert bound == set(declared_symbols())
+
+
+def test_abi_version():
+    import vdn_fp8._lib as L
+    m = re.search(r"#define VDN_FP8_ABI_VERSION (\d+)", open(HEADER).read())
+    assert L.load().vdn_fp8_abi_version() == int(m.group(1)) == L.ABI_VERSION
+
+
+def test_constants_match_header():
+    import vdn_fp8._lib as L
+    text = open(HEADER).read()
+    for name, value in (("VDN_FP8_OK", L.OK), ("VDN_FP8_EINVAL", L.EINVAL), ("VDN_FP8_ELAUNCH", L.ELAUNCH),
+                        ("VDN_FP8_EPI_NONE", L.EPI_NONE), ("VDN_FP8_EPI_GELU_TANH", L.EPI_GELU_TANH),
+                        ("VDN_FP8_EPI_GATE", L.EPI_GATE)):
+        assert int(re.search(rf"#define {name} (\d+)", text).group(1)) == value
+
+
+FAKE = 1 << 20        # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("call,needle", [
+    (lambda l: l.vdn_fp8_quantize_rows(FAKE, 4, 12, 12, FAKE, 12, FAKE, None), "multiples of 8"),
+    (lambda l: l.vdn_fp8_quantize_rows(FAKE, -1, 8, 8, FAKE, 8, FAKE, None), "negative"),
+    (lambda l: l.vdn_fp8_quantize_rows(None, 4, 8, 8, FAKE, 8, FAKE, None), "null"),
+    (lambda l: l.vdn_fp8_quantize_rows(FAKE + 8, 4, 8, 8, FAKE, 8, FAKE, None), "aligned"),
+    (lambda l: l.vdn_fp8_swiglu_quantize_rows(FAKE, 4, 8, 8, FAKE, 8, FAKE, None), "2K"),
+    (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 8, 8, FAKE, None, 4, 1.0, FAKE, 8, FAKE, None, None), "together"),
+    (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 32, 32, FAKE, FAKE, 200, 1.0, FAKE, 32, FAKE, None, None), "rank"),
+    (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 24, 24, FAKE, FAKE, 8, 1.0, FAKE, 24, FAKE, None, None), "K % 16"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 24, 32, 32, None, 0, None, None, 0, 0, None, 0, FAKE, 4, None), "multiple of 16"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 6, 32, 32, 32, None, 0, None, None, 0, 0, None, 0, FAKE, 8, None), "multiple of 4"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 7, None, None, 0, 0, None, 0, FAKE, 4, None), "epilogue"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 2, None, None, 0, 0, None, 0, FAKE, 4, None), "gate"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 16, 32, None, 0, None, None, 0, 0, None, 0, FAKE, 4, None), "ldx"),
+])
+def test_contract_violations_are_einval(call, needle):
+    import vdn_fp8._lib as L
+    lib = L.load()
+    assert call(lib) == L.EINVAL
+    assert needle in lib.vdn_fp8_last_error().decode()
+
+
+def test_empty_problems_are_no_ops():
+    import vdn_fp8._lib as L
+    lib = L.load()
+    assert lib.vdn_fp8_quantize_rows(None, 0, 8, 8, None, 8, None, None) == L.OK
+    assert lib.vdn_fp8_gemm(None, None, None, None, 0, 16, 32, 32, 32, None, 0, None, None, 0, 0, None, 0, None, 16, None) == L.OK
+    assert lib.vdn_fp8_requantize_weight(None, 0, 8, 8, None, None, 0, 1.0, None, 8, None, None, None) == L.OK
+
+
+def test_check_raises_reference_exception_types():
+    import vdn_fp8._lib as L
+    lib = L.load()
+    lib.vdn_fp8_quantize_rows(FAKE, 4, 12, 12, FAKE, 12, FAKE, None)
+    with pytest.raises(ValueError):
+        L.check(L.EINVAL, "quantize_rows")
+    with pytest.raises(L.Fp8LibraryError):
+        L.check(L.ELAUNCH, "gemm")

@@ -1,0 +1,271 @@
+"""Pins the CPU oracle (test infrastructure) before anything is compared with it.
+
+Each check is independent of the oracle's own code: torch's CPU casts (the library
+routines the reference's eager spellings call), a nearest-value brute force over the
+256 e4m3 codes, known answers probed from torch, closed forms and invariants.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import same_codes
+
+FP8 = torch.float8_e4m3fn
+
+
+def torch_e4m3(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(FP8).view(torch.uint8).numpy()
+
+
+def u16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------------
+# e4m3 / bf16 element conversions
+# ---------------------------------------------------------------------------------
+
+def test_e4m3_all_bf16_values_match_torch():
+    """Every bf16 pattern (all 65536), as binary32, encodes like torch's cast."""
+    x = O.bf16_decode(np.arange(1 << 16, dtype=np.uint32).astype(np.uint16))
+    assert np.all(same_codes(O.e4m3_encode(x), torch_e4m3(x)))
+
+
+def test_e4m3_rounding_midpoints_match_torch():
+    """Every midpoint between adjacent e4m3 values, and its binary32 neighbours: the
+    inputs where a wrong tie rule or an off-by-one exponent shows."""
+    vals = O.e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)   # 0 .. 448
+    mids = np.concatenate([(vals[:-1] + vals[1:]) / 2, [464.0]]).astype(np.float32)
+    near = np.concatenate([mids, np.nextafter(mids, 0), np.nextafter(mids, np.inf)])
+    near = np.concatenate([near, -near])
+    assert np.all(same_codes(O.e4m3_encode(near), torch_e4m3(near)))
+
+
+def test_e4m3_random_fp32_match_torch():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    assert np.all(same_codes(O.e4m3_encode(x), torch_e4m3(x)))
+
+
+def test_e4m3_brute_force_nearest():
+    """Round to the nearest of the 126 positive finite codes, ties to the even code,
+    magnitudes past the 448/NaN midpoint to NaN -- from the definition, on a dense
+    sample of binary32 values."""
+    table = O.e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # codes 0..0x7e
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.uniform(0, 470, 200_000), np.exp(rng.uniform(-25, 6.2, 200_000))]).astype(np.float32)
+    xd = x.astype(np.float64)
+    idx = np.searchsorted(table, xd)            # table[idx-1] < x <= table[idx]
+    lo = np.clip(idx - 1, 0, 125)
+    hi = np.clip(idx, 0, 126)
+    dlo, dhi = xd - table[lo], table[hi] - xd
+    pick = np.where(dlo < dhi, lo, np.where(dhi < dlo, hi, np.where(lo % 2 == 0, lo, hi)))
+    want = np.where(xd > 464.0, 0x7F, pick).astype(np.uint8)
+    want = np.where(xd == table[hi], hi, want).astype(np.uint8)
+    assert np.array_equal(O.e4m3_encode(x), want)
+
+
+@pytest.mark.parametrize("v,code", [(448.0, 0x7E), (463.9, 0x7E), (464.0, 0x7E), (470.0, 0x7F), (480.0, 0x7F),
+                                    (2.0 ** -9, 0x01), (2.0 ** -10, 0x00), (0.0013671875, 0x01), (1e-12, 0x00),
+                                    (-0.0, 0x80), (-1e-5, 0x80), (1.0, 0x38), (-2.0, 0xC0), (2.0 ** -6, 0x08)])
+def test_e4m3_known_answers(v, code):
+    """Known answers probed from torch's CPU cast in this container."""
+    assert O.e4m3_encode(np.array([v], np.float32))[0] == code
+
+
+def test_e4m3_decode_table():
+    c = np.arange(256, dtype=np.uint8)
+    f = O.e4m3_decode(c)
+    ref = torch.from_numpy(c.copy()).view(FP8).float().numpy()
+    assert np.array_equal(np.isnan(f), np.isnan(ref))
+    ok = ~np.isnan(f)
+    assert np.array_equal(f[ok].view(np.uint32), ref[ok].view(np.uint32))
+
+
+def test_bf16_encode_matches_torch():
+    rng = np.random.default_rng(2)
+    bits = rng.integers(0, 2 ** 32, size=1_000_000, dtype=np.uint64).astype(np.uint32)
+    # add every exact tie and its neighbours in a few binades
+    ties = (np.arange(1 << 16, dtype=np.uint32) << 16) | 0x8000
+    x = np.concatenate([bits, ties, ties + 1, ties - 1]).view(np.float32)
+    x = x[~np.isnan(x)]
+    got = O.bf16_encode(x)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------------
+# the quantizers against the reference's eager spellings in torch
+# ---------------------------------------------------------------------------------
+
+def rows_reference(x):
+    """quantize_rows_reference (fp8_linear.py:132-135), torch CPU ops."""
+    scale = (x.float().abs().amax(dim=1, keepdim=True) / 448.0).clamp_min(1e-12)
+    return (x.float() / scale).to(FP8), scale
+
+
+def weight_reference(w):
+    """Rowwise branch of Fp8Linear.__init__ (fp8_linear.py:262-267), torch CPU ops."""
+    scale = (w.abs().amax(dim=1, keepdim=True).float() / 448.0).clamp_min(1e-12)
+    return (w / scale.to(w.dtype)).to(FP8), scale.reshape(1, -1)
+
+
+def _rows_cases():
+    g = torch.Generator().manual_seed(3)
+    yield torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    x = torch.randn(32, 5120, generator=g)
+    x[:, torch.randperm(5120, generator=g)[:5]] *= 20
+    yield x.to(torch.bfloat16)
+    yield (torch.randn(8, 640, generator=g) * 1e-14).to(torch.bfloat16)          # below the floor
+    yield (torch.randn(8, 640, generator=g) * 1e-38).to(torch.bfloat16)          # subnormals
+    yield torch.zeros(2, 64, dtype=torch.bfloat16)
+    yield -torch.zeros(2, 64, dtype=torch.bfloat16)
+    yield (torch.rand(16, 2048, generator=g) * 3e38).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", range(7))
+def test_quantize_rows_matches_eager(case):
+    x = list(_rows_cases())[case]
+    q, s = O.quantize_rows(u16(x))
+    rq, rs = rows_reference(x)
+    assert np.array_equal(q, rq.view(torch.uint8).numpy())
+    assert np.array_equal(s.view(np.uint32), rs.reshape(-1).numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("case", range(7))
+def test_quantize_weight_matches_eager(case):
+    w = list(_rows_cases())[case]
+    q, s = O.quantize_weight(u16(w))
+    rq, rs = weight_reference(w)
+    assert np.array_equal(q, rq.view(torch.uint8).numpy())
+    assert np.array_equal(s.view(np.uint32), rs.reshape(-1).numpy().view(np.uint32))
+
+
+def test_quantize_weight_double_rounding_matters():
+    """A planted mistake must be caught: a single rounding (binary32 quotient straight
+    to e4m3, skipping the bf16 round) differs from the reference's codes on ordinary
+    weights, so the pinning above discriminates."""
+    g = torch.Generator().manual_seed(4)
+    w = (torch.randn(64, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    rq, rs = weight_reference(w)
+    single = (w.float() / rs.reshape(-1, 1).to(torch.bfloat16).float()).to(FP8)
+    assert (single.view(torch.uint8) != rq.view(torch.uint8)).any()
+
+
+def test_quantize_rows_invariants():
+    rng = np.random.default_rng(5)
+    x = O.bf16_encode(rng.standard_normal((256, 512), dtype=np.float32) * rng.uniform(1e-3, 1e3, (256, 1)))
+    q, s = O.quantize_rows(x)
+    xf = O.bf16_decode(x)
+    assert np.all(s >= np.float32(1e-12))
+    mags = np.abs(xf).max(axis=1)
+    arg = np.abs(xf).argmax(axis=1)
+    # the row maximum maps to +-448
+    assert np.all(q[np.arange(256), arg] & 0x7F == 0x7E)
+    assert np.all(O.e4m3_decode(q) * np.sign(xf) >= 0)            # sign kept
+    assert np.allclose(s, mags / 448.0, rtol=1e-7)
+
+
+def test_swiglu_oracle_close_to_eager():
+    """parity unpinned beyond tolerance: sigmoid is transcendental. Against torch's
+    eager a * silu(g) in fp32: scales within 1e-6, codes within one step."""
+    g = torch.Generator().manual_seed(6)
+    h = (torch.randn(32, 2 * 1024, generator=g) * 2).to(torch.bfloat16)
+    q, s = O.swiglu_quantize_rows(u16(h))
+    a, gt = h.float().chunk(2, dim=1)
+    act = a * gt * torch.sigmoid(gt)
+    rs = (act.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    rq = (act / rs[:, None]).to(FP8).view(torch.uint8).numpy()
+    np.testing.assert_allclose(s, rs.numpy(), rtol=1e-6)
+    assert np.mean(q != rq) < 1e-3
+    assert np.max(np.abs(q.astype(int) - rq.astype(int))) <= 1
+
+
+# ---------------------------------------------------------------------------------
+# LoRA merge
+# ---------------------------------------------------------------------------------
+
+def test_lora_merge_against_torch_fp32_matmul():
+    g = torch.Generator().manual_seed(7)
+    w = (torch.randn(96, 512, generator=g) * 0.02).to(torch.bfloat16)
+    a = (torch.randn(32, 512, generator=g) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(96, 32, generator=g) * 0.05).to(torch.bfloat16)
+    for scale in (1.0, 0.5):
+        ref = w.clone()
+        ref.add_(((b.float() @ a.float()) * scale).to(torch.bfloat16))
+        got = O.lora_merge(u16(w), u16(a), u16(b), scale)
+        d = np.abs(got.astype(np.int32) - u16(ref).astype(np.int32))
+        assert np.mean(d != 0) < 1e-2          # fp32 summation order only
+        gv, rv = O.bf16_decode(got), ref.float().numpy()
+        assert np.max(np.abs(gv - rv)) <= 2.0 ** -14   # one bf16 ulp at the operands' scale
+
+
+def test_lora_merge_exact_small_integers():
+    """Brute force with a closed form: integer factors give exact sums; the merged
+    weight is bf16(w + bf16(scale * (B @ A)))."""
+    rng = np.random.default_rng(8)
+    a = rng.integers(-3, 4, (8, 40)).astype(np.float32)
+    b = rng.integers(-3, 4, (24, 8)).astype(np.float32)
+    w = rng.integers(-50, 50, (24, 40)).astype(np.float32)
+    got = O.bf16_decode(O.lora_merge(O.bf16_encode(w), O.bf16_encode(a), O.bf16_encode(b), 2.0))
+    assert np.array_equal(got, w + 2.0 * (b @ a))
+
+
+# ---------------------------------------------------------------------------------
+# dequantized matmul and epilogues
+# ---------------------------------------------------------------------------------
+
+def test_dequant_linear_closed_form():
+    """Identity-like weights: out = x * sx * sw exactly before rounding."""
+    rng = np.random.default_rng(9)
+    qx = O.e4m3_encode(rng.integers(-8, 9, (16, 32)).astype(np.float32))
+    qw = O.e4m3_encode(np.eye(32, dtype=np.float32))
+    sx = np.full(16, 0.5, np.float32)
+    sw = np.full(32, 0.25, np.float32)
+    out = O.dequant_linear(qx, sx, qw, sw, rounding="none")
+    assert np.array_equal(out, O.e4m3_decode(qx).astype(np.float64) * 0.125)
+
+
+def test_gelu_tanh_matches_torch():
+    v = np.linspace(-8, 8, 10001)
+    ref = torch.nn.functional.gelu(torch.from_numpy(v), approximate="tanh").numpy()
+    np.testing.assert_allclose(O.gelu_tanh(v), ref, rtol=1e-12, atol=1e-14)
+
+
+def test_gate_epilogue_matches_post_ref():
+    """residual + gate.index_select(0, idx) * out (fused_block.py:47-49)."""
+    rng = np.random.default_rng(10)
+    qx = O.e4m3_encode(rng.standard_normal((12, 64)).astype(np.float32))
+    qw = O.e4m3_encode(rng.standard_normal((16, 64)).astype(np.float32))
+    sx, sw = np.ones(12, np.float32), np.full(16, 0.1, np.float32)
+    gate = O.bf16_encode(rng.uniform(0, 2, (3, 16)).astype(np.float32))
+    idx = rng.integers(0, 3, 12)
+    res = O.bf16_encode(rng.standard_normal((12, 16)).astype(np.float32))
+    base = O.dequant_linear(qx, sx, qw, sw, rounding="none")
+    got = O.dequant_linear(qx, sx, qw, sw, epilogue="gate", gate=gate, gate_index=idx, residual=res, rounding="none")
+    want = O.bf16_decode(res) + O.bf16_decode(gate)[idx] * base
+    np.testing.assert_allclose(got, want, rtol=1e-12)
+
+
+def test_reference_rounding_points():
+    """rounding="reference" is bf16(bf16(matmul) + bias): planted single rounding
+    differs from it somewhere, so the two spellings are distinguished."""
+    rng = np.random.default_rng(11)
+    qx = O.e4m3_encode(rng.standard_normal((64, 256)).astype(np.float32))
+    qw = O.e4m3_encode(rng.standard_normal((64, 256)).astype(np.float32))
+    sx, sw = np.full(64, 0.01, np.float32), np.full(64, 0.02, np.float32)
+    bias = O.bf16_encode(rng.standard_normal(64).astype(np.float32))
+    ref = O.dequant_linear(qx, sx, qw, sw, bias=bias)
+    raw = O.dequant_linear(qx, sx, qw, sw, bias=bias, rounding="none")
+    single = O.bf16_decode(O.bf16_encode(raw.astype(np.float32)))
+    assert np.array_equal(ref, O.bf16_decode(O.bf16_encode(ref.astype(np.float32))))   # bf16 values
+    assert np.any(ref != single)
+    assert O.rel_l2(ref, raw) < 3e-3

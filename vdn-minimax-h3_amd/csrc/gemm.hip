@@ -1,0 +1,461 @@
+// fp8 x fp8 GEMM with per-token x per-output-channel dequantization and a
+// fused bias / GELU(tanh) / AdaLN-gate epilogue, for gfx950 (MI355X).
+//
+//   v         = bf16(x_scale[m] * w_scale[n] * sum_k xq[m][k] wq[n][k])
+//   v         = bf16(v + bias[n])                          (with a bias)
+//   out[m][n] = bf16(epi(v))                               (none / GELU(tanh) / gate)
+// rounding to bf16 where the reference's op sequence does (_scaled_mm with
+// out_dtype=bf16, the bf16 bias add, then the epilogue on the bf16 tensor).
+//
+// Both operands are K-contiguous (xq [M, K], wq [N, K]), the "TN" layout of
+// torch._scaled_mm(x_fp8, weight_fp8.t()) in the reference (fp8_linear.py:272).
+//
+// Main kernel (K % 128 == 0). A workgroup of 4 wavefronts computes a 256 (m) x
+// 256 (n) output tile; each wave owns a 128 x 128 quadrant as 4 x 4
+// v_mfma_f32_32x32x64_f8f6f4 tiles (256 fp32 accumulators per lane, in AGPRs).
+// K advances in 128-byte blocks through two LDS stages (X and W tiles of 256
+// rows x 128 bytes: 64 KiB a stage). Global -> LDS copies bypass VGPRs
+// (buffer_load_dwordx4 ... lds) and move whole 128-byte rows -- half-line
+// copies stream at two thirds of the rate on this part. Each block is
+// consumed as two half-steps of 16 MFMAs; the next half-step's operand
+// fragments are read from LDS into a second VGPR set while the current
+// half-step's MFMAs run, and the copies of block j+2 are issued as soon as
+// every wave is done with block j (one barrier per block).
+// LDS rows are 128 bytes; the 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7),
+// so the 16 rows a 16-lane group reads hit 16 distinct 16-byte bank groups of
+// gfx950's 64 banks (no conflicts for ds_read_b128).
+//
+// MFMA orientation: the instruction's A operand is the W tile (its rows are
+// output channels n) and its B operand the X tile (columns are tokens m), so
+// each lane's accumulators come in runs of 4 consecutive n of one m: the
+// epilogue stores 8 bytes (4 bf16) per lane.
+//
+// Tile order: workgroup b runs on XCD b % 8; tiles are renumbered so each XCD
+// walks a contiguous run of the tile space, grouped 8 m-tiles at a time, which
+// keeps the X and W slices its 32 CUs share resident in that XCD's L2.
+//
+// K % 128 != 0 goes to a second kernel (BK = 128, 16x16x128 MFMA, two stages)
+// whose last step is filled through VGPRs with zeros past K.
+#include <stdint.h>
+
+#include "vdn_common.h"
+
+namespace vdn {
+namespace {
+
+constexpr int BM = 256;        // tokens per tile
+constexpr int BN = 256;        // output channels per tile
+constexpr int kThreads = 256;  // 4 wavefronts, 2 (n) x 2 (m), 128 x 128 each
+constexpr int kGroupM = 8;
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+struct GemmArgs {
+    const uint8_t* xq;
+    const float* sx;
+    const uint8_t* wq;
+    const float* sw;
+    int64_t M, N, K, ldx, ldw;
+    const uint16_t* bias;
+    const uint16_t* gate;
+    const int32_t* gate_index;
+    int64_t gate_rows, ldgate;
+    const uint16_t* residual;
+    int64_t ldres;
+    uint16_t* out;
+    int64_t ldo;
+    int tiles_m, tiles_n;
+};
+
+// gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3)
+__device__ __forceinline__ float gelu_tanh(float v)
+{
+    const float u2 = 1.5957691216057308f * (v + 0.044715f * v * v * v);  // 2u
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-u2));
+}
+
+// Renumbers workgroup b so that XCD (b % 8) gets a contiguous run of tiles,
+// then maps the run index to (tile_m, tile_n) in groups of kGroupM m-tiles.
+__device__ __forceinline__ void tile_coords(int b, int tiles_m, int tiles_n, int& tm, int& tn)
+{
+    const int T = tiles_m * tiles_n;
+    const int q = T / 8, r = T % 8, xcd = b % 8, local = b / 8;
+    const int t = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+    const int group = kGroupM * tiles_n;
+    const int first_m = (t / group) * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    tm = first_m + (t % group) % gsize;
+    tn = (t % group) / gsize;
+}
+
+// Epilogue for 4 consecutive output channels n .. n+3 of token m: the
+// reference's rounding points, then one 8-byte store.
+template <int EPI>
+__device__ __forceinline__ void store4(const GemmArgs& p, int64_t m, int64_t n, const float* acc, float sxm,
+                                       const uint16_t* grow)
+{
+    const float4 sw = *reinterpret_cast<const float4*>(p.sw + n);
+    const float swv[4] = {sw.x, sw.y, sw.z, sw.w};
+    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.bias) {
+        const uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
+        bv[0] = bf16_lo(b.x); bv[1] = bf16_hi(b.x); bv[2] = bf16_lo(b.y); bv[3] = bf16_hi(b.y);
+    }
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[e] = round_bf16(acc[e] * (sxm * swv[e]));
+        if (p.bias) v[e] = round_bf16(v[e] + bv[e]);
+    }
+    if (EPI == VDN_FP8_EPI_GELU_TANH) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+    } else if (EPI == VDN_FP8_EPI_GATE) {
+        const uint2 gv = *reinterpret_cast<const uint2*>(grow + n);
+        v[0] *= bf16_lo(gv.x); v[1] *= bf16_hi(gv.x); v[2] *= bf16_lo(gv.y); v[3] *= bf16_hi(gv.y);
+        if (p.residual) {
+            const uint2 rv = *reinterpret_cast<const uint2*>(p.residual + m * p.ldres + n);
+            v[0] += bf16_lo(rv.x); v[1] += bf16_hi(rv.x); v[2] += bf16_lo(rv.y); v[3] += bf16_hi(rv.y);
+        }
+    }
+    *reinterpret_cast<uint2*>(p.out + m * p.ldo + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+template <int EPI>
+__device__ __forceinline__ const uint16_t* gate_row(const GemmArgs& p, int64_t m)
+{
+    if (EPI != VDN_FP8_EPI_GATE) return nullptr;
+    const int64_t gi = p.gate_index ? min(max((int64_t)p.gate_index[m], (int64_t)0), p.gate_rows - 1) : 0;
+    return p.gate + gi * p.ldgate;
+}
+
+// Buffer descriptor (raw, 32-bit data format, gfx9 family) over the valid rows
+// of a tile: rows past M (or N) read as zeros. Wave-uniform, so in SGPRs.
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ i32x4_t tile_rsrc_words(const uint8_t* base, int64_t rows, int64_t ld)
+{
+    const uint64_t a = (uint64_t)base;
+    const int64_t bytes = min(min(rows, (int64_t)256) * ld, (int64_t)0x7fffffff);
+    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu)),
+                   __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), kRsrcWord3};
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint8_t* base, int64_t rows, int64_t ld)
+{
+    const int64_t bytes = min(rows, (int64_t)256) * ld;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)min(bytes, (int64_t)0x7fffffff), kRsrcWord3);
+}
+
+// One wave-wide 16-byte-per-lane copy global -> LDS: lane L's 16 bytes at
+// buffer offset voff + soff land at LDS byte lds + 16 L. Written as inline
+// assembly so that the compiler does not treat every later LDS read as
+// dependent on it (it would wait for all such copies, serializing the
+// pipeline); the kernel waits on vmcnt itself. M0 carries the LDS address and
+// is restored afterwards; s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff)
+{
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+        : "memory");
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | (0 << 8) | ((vm >> 4) << 14); }
+
+// ---------------------------------------------------------------------------
+// main kernel: K % 128 == 0
+// ---------------------------------------------------------------------------
+namespace mainloop {
+constexpr int BK = 128;                     // K bytes per block (one LDS stage)
+constexpr int kStage = (BM + BN) * BK;      // 64 KiB: X tile, then W tile
+constexpr int kCopies = BM * BK / 1024 / 4; // 1 KiB copies per wave per tile per block (8)
+
+// Row r, 16-byte chunk c (0..7) of a tile sits at chunk c ^ ((r >> 1) & 7) of
+// its 128-byte LDS row.
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
+}  // namespace mainloop
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemm_fp8(GemmArgs p)
+{
+    using namespace mainloop;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1, wm = wave >> 1;
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int nk = (int)(p.K / BK);
+
+    // Copies: this wave fills rows 64 wave .. 64 wave + 63 of each tile, 8 rows
+    // (1 KiB) per copy. Lane L lands at row +L/8, physical chunk L%8, so it
+    // fetches logical chunk (L%8) ^ ((row >> 1) & 7), row = 64 wave + 8 i + L/8.
+    const i32x4_t xr = tile_rsrc_words(p.xq + m0 * p.ldx, p.M - m0, p.ldx);
+    const i32x4_t wr = tile_rsrc_words(p.wq + n0 * p.ldw, p.N - n0, p.ldw);
+    uint32_t xoff[kCopies], woff[kCopies];
+#pragma unroll
+    for (int i = 0; i < kCopies; ++i) {
+        const int r = 64 * wave + 8 * i + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        xoff[i] = (uint32_t)(r * p.ldx) + c * 16;
+        woff[i] = (uint32_t)(r * p.ldw) + c * 16;
+    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    // Copies of block j into stage j % 2. Blocks past the end still issue
+    // their copies with an out-of-range offset (the buffer returns zeros and no
+    // memory is read), keeping the loop free of data-dependent branches.
+    auto issue = [&](int j) {
+        const uint32_t st = lds_base + (uint32_t)(j & 1) * kStage;
+        const uint32_t kb = (uint32_t)j * BK;
+        const bool live = j < nk;
+#pragma unroll
+        for (int i = 0; i < kCopies; ++i) {
+            copy16_to_lds(xr, st + (64 * wave + 8 * i) * BK, live ? xoff[i] : 0x80000000u, kb);
+            copy16_to_lds(wr, st + BM * BK + (64 * wave + 8 * i) * BK, live ? woff[i] : 0x80000000u, kb);
+        }
+    };
+
+    // Fragments of half h (k bytes 64 h .. 64 h + 63) of block j: lane reads row
+    // (base + lane % 32), k bytes 64 h + 32 (lane / 32) .. +31, as two 16-byte chunks.
+    const int frow = lane & 31, fh = lane >> 5;
+    auto read_frag = [&](const uint8_t* s, int row, int h) -> i32x8_t {
+        const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh));
+        const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh + 1));
+        return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+    auto read_half = [&](int j, int h, i32x8_t* wf, i32x8_t* xf) {
+        const uint8_t* st = smem + (j & 1) * kStage;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wf[t] = read_frag(st + BM * BK, wn * 128 + 32 * t + frow, h);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xf[u] = read_frag(st, wm * 128 + 32 * u + frow, h);
+    };
+
+    f32x16_t acc[4][4] = {};
+    auto mfmas = [&](const i32x8_t* wf, const i32x8_t* xf) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc[t][u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t], xf[u], acc[t][u], 0, 0, 0, 0, 0, 0);
+    };
+
+    // Prologue: blocks 0 and 1 in flight; wait for block 0, read its first half.
+    // The s_nop keeps 5 wait states between the v_readfirstlane writes of the
+    // descriptors and their first use by a buffer load (an SGPR hazard that the
+    // compiler does not see through inline assembly).
+    asm volatile("s_nop 4");
+    issue(0);
+    issue(1);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * kCopies));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    i32x8_t w0[4], x0[4], w1[4], x1[4];
+    read_half(0, 0, w0, x0);
+
+    // One trip per block j, two MFMA half-steps:
+    //  half 0: read half 1 of block j into set 1 while the MFMAs use set 0;
+    //  half 1: wait for block j+1 (and for this wave's reads of block j), meet
+    //          the other waves, refill stage j % 2 with block j+2, read half 0
+    //          of block j+1 into set 0 while the MFMAs use set 1.
+    // Block j+2's copies have two half-steps (32 MFMAs) to land. The scheduling
+    // groups put each half-step's 16 LDS reads ahead of its 16 MFMAs.
+    for (int j = 0; j < nk; ++j) {
+        read_half(j, 1, w1, x1);
+        mfmas(w0, x0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        issue(j + 2);
+        read_half(j + 1, 0, w0, x0);
+        mfmas(w1, x1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // No copy may still be writing LDS when the workgroup ends.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+
+    // Epilogue: acc[t][u][r] is n = n0 + wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4,
+    // m = m0 + wm*128 + 32 u + lane%32.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t m = m0 + wm * 128 + 32 * u + frow;
+        if (m >= p.M) continue;
+        const float sxm = p.sx[m];
+        const uint16_t* grow = gate_row<EPI>(p, m);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t n = n0 + wn * 128 + 32 * t + 8 * q + 4 * fh;
+                if (n >= p.N) continue;
+                const float a4[4] = {acc[t][u][4 * q], acc[t][u][4 * q + 1], acc[t][u][4 * q + 2], acc[t][u][4 * q + 3]};
+                store4<EPI>(p, m, n, a4, sxm, grow);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// tail kernel: K % 128 != 0 (K % 16 == 0)
+// ---------------------------------------------------------------------------
+namespace tailloop {
+constexpr int BK = 128;
+constexpr int kStage = (BM + BN) * BK;
+constexpr int kChunks = BM * BK / 16 / kThreads;  // 8
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
+}  // namespace tailloop
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemm_fp8_ktail(GemmArgs p)
+{
+    using namespace tailloop;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1, wm = wave >> 1;
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int nk = (int)((p.K + BK - 1) / BK);
+
+    // Thread copies chunk q = tid + 256 i: row q / 8, 16-byte chunk q % 8, through
+    // VGPRs (zero past K), into the swizzled LDS layout.
+    const __amdgpu_buffer_rsrc_t xr = tile_rsrc(p.xq + m0 * p.ldx, p.M - m0, p.ldx);
+    const __amdgpu_buffer_rsrc_t wr = tile_rsrc(p.wq + n0 * p.ldw, p.N - n0, p.ldw);
+    const int srow = tid >> 3, schunk = tid & 7;
+    auto fill = [&](uint8_t* st, int kt) {
+        const uint32_t kb = (uint32_t)kt * BK;
+        const bool in = (int64_t)kb + schunk * 16 < p.K;
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int r = srow + 32 * i;
+            uint4 vx = z, vw = z;
+            if (in) {
+                vx = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)(r * p.ldx) + schunk * 16, kb, 0));
+                vw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)(r * p.ldw) + schunk * 16, kb, 0));
+            }
+            *reinterpret_cast<uint4*>(st + lds_off(r, schunk)) = vx;
+            *reinterpret_cast<uint4*>(st + BM * BK + lds_off(r, schunk)) = vw;
+        }
+    };
+
+    f32x4_t acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int frow = lane & 15, fg = lane >> 4;
+    auto read_frag = [&](const uint8_t* s, int row) -> i32x8_t {
+        const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg));
+        const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg + 1));
+        return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+    for (int kt = 0; kt < nk; ++kt) {
+        uint8_t* const st = smem + (kt & 1) * kStage;
+        fill(st, kt);
+        __syncthreads();
+        i32x8_t wf[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wf[i] = read_frag(st + BM * BK, wn * 128 + i * 16 + frow);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const i32x8_t xf = read_frag(st, wm * 128 + j * 16 + frow);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf, acc[i][j], 0, 0, 0, 0, 0, 0);
+        }
+    }
+
+    // Epilogue: lane holds n = n0 + wn*128 + 16 i + 4 (lane/16) + e, m = m0 + wm*128 + 16 j + lane%16.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t m = m0 + wm * 128 + j * 16 + frow;
+        if (m >= p.M) continue;
+        const float sxm = p.sx[m];
+        const uint16_t* grow = gate_row<EPI>(p, m);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t n = n0 + wn * 128 + i * 16 + 4 * fg;
+            if (n >= p.N) continue;
+            const float a4[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            store4<EPI>(p, m, n, a4, sxm, grow);
+        }
+    }
+}
+
+bool aligned(const void* q, uintptr_t a) { return ((uintptr_t)q % a) == 0; }
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, int64_t M,
+                            int64_t N, int64_t K, int64_t ldx, int64_t ldw, const void* bias, int epilogue,
+                            const void* gate, const int32_t* gate_index, int64_t gate_rows, int64_t ldgate,
+                            const void* residual, int64_t ldres, void* out, int64_t ldo, hipStream_t stream)
+{
+    if (M < 0 || N < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "gemm: negative shape");
+    if (M == 0 || N == 0) return VDN_FP8_OK;
+    if (K == 0 || K % 16) return set_error(VDN_FP8_EINVAL, "gemm: K must be a positive multiple of 16 (K=%lld)", (long long)K);
+    if (N % 4) return set_error(VDN_FP8_EINVAL, "gemm: N must be a multiple of 4 (N=%lld)", (long long)N);
+    if (!xq || !wq || !x_scale || !w_scale || !out) return set_error(VDN_FP8_EINVAL, "gemm: null pointer");
+    if (ldx < K || ldw < K || ldo < N || ldx % 16 || ldw % 16 || ldo % 4)
+        return set_error(VDN_FP8_EINVAL, "gemm: need ldx, ldw >= K and multiples of 16, ldo >= N and a multiple of 4");
+    if (ldx * 256 > (int64_t)0x7fffffff || ldw * 256 > (int64_t)0x7fffffff)
+        return set_error(VDN_FP8_EINVAL, "gemm: row stride too large (256 rows must span < 2 GiB)");
+    if (!aligned(xq, 16) || !aligned(wq, 16) || !aligned(out, 8) || !aligned(w_scale, 16) || (bias && !aligned(bias, 8)))
+        return set_error(VDN_FP8_EINVAL, "gemm: misaligned operand (xq, wq 16 B; w_scale 16 B; out, bias 8 B)");
+    if (epilogue == VDN_FP8_EPI_GATE) {
+        if (!gate || gate_rows < 1) return set_error(VDN_FP8_EINVAL, "gemm: the gate epilogue needs a gate table of >= 1 row");
+        if (ldgate < N || ldgate % 4 || !aligned(gate, 8)) return set_error(VDN_FP8_EINVAL, "gemm: gate rows must be >= N and 8-byte aligned");
+        if (residual && (ldres < N || ldres % 4 || !aligned(residual, 8)))
+            return set_error(VDN_FP8_EINVAL, "gemm: residual rows must be >= N and 8-byte aligned");
+    } else if (epilogue != VDN_FP8_EPI_NONE && epilogue != VDN_FP8_EPI_GELU_TANH) {
+        return set_error(VDN_FP8_EINVAL, "gemm: unknown epilogue %d", epilogue);
+    }
+    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if (tiles_m * tiles_n > (int64_t)INT32_MAX / 2) return set_error(VDN_FP8_EINVAL, "gemm: problem too large");
+    GemmArgs p{(const uint8_t*)xq, x_scale, (const uint8_t*)wq, w_scale, M, N, K, ldx, ldw,
+               (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
+               (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n};
+    const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
+    const bool main = (K % mainloop::BK) == 0;
+#define VDN_LAUNCH(E)                                                                   \
+    do {                                                                                \
+        if (main) hipLaunchKernelGGL((k_gemm_fp8<E>), grid, block, 0, stream, p);       \
+        else hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);      \
+    } while (0)
+    switch (epilogue) {
+        case VDN_FP8_EPI_NONE: VDN_LAUNCH(VDN_FP8_EPI_NONE); break;
+        case VDN_FP8_EPI_GELU_TANH: VDN_LAUNCH(VDN_FP8_EPI_GELU_TANH); break;
+        default: VDN_LAUNCH(VDN_FP8_EPI_GATE); break;
+    }
+#undef VDN_LAUNCH
+    return check_launch("gemm");
+}

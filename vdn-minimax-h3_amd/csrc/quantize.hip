@@ -1,0 +1,310 @@
+// Row quantizers for the fp8 linear path (gfx950):
+//   - per-token activation quantization      (vdn_fp8_quantize_rows)
+//   - fused SwiGLU + per-token quantization  (vdn_fp8_swiglu_quantize_rows)
+//   - rowwise weight quantization, no LoRA   (vdn_fp8_requantize_weight)
+//
+// All three are HBM-bound: 2 bytes in and 1 byte out per element plus 4 bytes
+// of scale per row. One wavefront owns one row and keeps the whole row in
+// VGPRs between the absmax sweep and the scaled cast, so every input byte is
+// read from HBM exactly once (the reference's Triton kernel reads each row
+// twice, fp8_linear.py:21-23,70-78). Loads are 16 bytes per lane and
+// consecutive lanes read consecutive 16-byte chunks (a wave reads 1 KiB
+// contiguous per instruction); stores are 8 bytes per lane, likewise
+// contiguous.
+#include <stdint.h>
+
+#include "vdn_common.h"
+
+namespace vdn {
+namespace {
+
+constexpr int kWavesPerBlock = 4;  // rows per workgroup
+constexpr int kLanes = 64;
+
+// Quotient of the quantizers. kWeight selects the weight path's double
+// rounding (binary32 quotient by bf16(scale), rounded to bf16). kExact uses
+// the IEEE division, for the rows whose scale is not finite (a row holding
+// inf or NaN), where the reciprocal form does not apply.
+template <bool kWeight, bool kExact>
+__device__ __forceinline__ float quotient(float x, float s, float r)
+{
+    float q = kExact ? x / s : div_by_scale(x, s, r);
+    return kWeight ? round_bf16(q) : q;
+}
+
+// Converts one 16-byte chunk (8 bf16) to 8 codes.
+template <bool kWeight, bool kExact>
+__device__ __forceinline__ uint2 quantize_chunk(uint4 v, float s, float r)
+{
+    uint2 out;
+    out.x = pack_e4m3x4(quotient<kWeight, kExact>(bf16_lo(v.x), s, r),
+                        quotient<kWeight, kExact>(bf16_hi(v.x), s, r),
+                        quotient<kWeight, kExact>(bf16_lo(v.y), s, r),
+                        quotient<kWeight, kExact>(bf16_hi(v.y), s, r));
+    out.y = pack_e4m3x4(quotient<kWeight, kExact>(bf16_lo(v.z), s, r),
+                        quotient<kWeight, kExact>(bf16_hi(v.z), s, r),
+                        quotient<kWeight, kExact>(bf16_lo(v.w), s, r),
+                        quotient<kWeight, kExact>(bf16_hi(v.w), s, r));
+    return out;
+}
+
+// CPL = 16-byte chunks held per lane; the row has K/8 chunks, CPL*64 >= K/8.
+template <int CPL, bool kWeight>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= M) return;
+    const int nch = (int)(K >> 3);
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+
+    uint4 v[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        v[c] = (idx < nch) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t m2 = 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        m2 = absmax_bf16x2(m2, v[c].x);
+        m2 = absmax_bf16x2(m2, v[c].y);
+        m2 = absmax_bf16x2(m2, v[c].z);
+        m2 = absmax_bf16x2(m2, v[c].w);
+    }
+    const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
+    if (lane == 0) scale_out[row] = scale;
+    const float sdiv = kWeight ? round_bf16(scale) : scale;
+    const float r = 1.0f / sdiv;
+
+    uint2* yr = reinterpret_cast<uint2*>(y + row * ldy);
+    if (__builtin_isfinite(sdiv)) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + kLanes * c;
+            if (idx < nch) yr[idx] = quantize_chunk<kWeight, false>(v[c], sdiv, r);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + kLanes * c;
+            if (idx < nch) yr[idx] = quantize_chunk<kWeight, true>(v[c], sdiv, r);
+        }
+    }
+}
+
+// Rows wider than 64*32 chunks (K > 16384): two sweeps, the second re-reads
+// the row (from L2 for all but the widest rows).
+template <bool kWeight>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant_wide(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= M) return;
+    const int64_t nch = K >> 3;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    uint32_t m2 = 0;
+    for (int64_t idx = lane; idx < nch; idx += kLanes) {
+        uint4 v = xr[idx];
+        m2 = absmax_bf16x2(m2, v.x);
+        m2 = absmax_bf16x2(m2, v.y);
+        m2 = absmax_bf16x2(m2, v.z);
+        m2 = absmax_bf16x2(m2, v.w);
+    }
+    const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
+    if (lane == 0) scale_out[row] = scale;
+    const float sdiv = kWeight ? round_bf16(scale) : scale;
+    const float r = 1.0f / sdiv;
+    uint2* yr = reinterpret_cast<uint2*>(y + row * ldy);
+    if (__builtin_isfinite(sdiv)) {
+        for (int64_t idx = lane; idx < nch; idx += kLanes) yr[idx] = quantize_chunk<kWeight, false>(xr[idx], sdiv, r);
+    } else {
+        for (int64_t idx = lane; idx < nch; idx += kLanes) yr[idx] = quantize_chunk<kWeight, true>(xr[idx], sdiv, r);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU + quantize
+// ---------------------------------------------------------------------------
+
+// a * g * sigmoid(g) in binary32 (the reference's Triton body, fp8_linear.py:88,96).
+__device__ __forceinline__ float swiglu(float a, float g)
+{
+    return a * g * __fdividef(1.0f, 1.0f + __expf(-g));
+}
+
+template <int CPL>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant(
+    const uint16_t* __restrict__ h, int64_t M, int64_t K, int64_t ldh,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= M) return;
+    const int nch = (int)(K >> 3);
+    const uint4* ar = reinterpret_cast<const uint4*>(h + row * ldh);
+    const uint4* gr = reinterpret_cast<const uint4*>(h + row * ldh + K);
+
+    float act[CPL][8];
+    float amax = 0.0f;
+    bool nan_seen = false;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        uint4 a = make_uint4(0u, 0u, 0u, 0u), g = a;
+        if (idx < nch) { a = ar[idx]; g = gr[idx]; }
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            act[c][2 * j] = swiglu(bf16_lo(aw[j]), bf16_lo(gw[j]));
+            act[c][2 * j + 1] = swiglu(bf16_hi(aw[j]), bf16_hi(gw[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            nan_seen |= __builtin_isnan(act[c][j]);
+            amax = fmaxf(amax, fabsf(act[c][j]));
+        }
+    }
+    // Magnitudes are non-negative, so their binary32 patterns order like
+    // unsigned integers; a NaN anywhere in the row makes the scale NaN.
+    uint32_t mbits = wave_max_u32(nan_seen ? 0x7fc00000u : __float_as_uint(amax));
+    const float scale = row_scale(__uint_as_float(mbits));
+    if (lane == 0) scale_out[row] = scale;
+    const float r = 1.0f / scale;
+    const bool finite = __builtin_isfinite(scale);
+
+    uint2* yr = reinterpret_cast<uint2*>(y + row * ldy);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        if (idx >= nch) continue;
+        float q[8];
+        if (finite) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false, false>(act[c][j], scale, r);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false, true>(act[c][j], scale, r);
+        }
+        yr[idx] = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
+    }
+}
+
+template <bool kWeight>
+void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t K,
+                     int64_t ldx, uint8_t* y, int64_t ldy, float* s)
+{
+    const dim3 block(kWavesPerBlock * kLanes);
+#define VDN_CASE(n)                                                                           \
+    case n: hipLaunchKernelGGL((k_rowquant<n, kWeight>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        return;
+    switch (cpl) {
+        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
+        VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
+        default: hipLaunchKernelGGL((k_rowquant_wide<kWeight>), grid, block, 0, st, x, M, K, ldx, y, ldy, s);
+    }
+#undef VDN_CASE
+}
+
+// Smallest instantiated chunks-per-lane that covers nch chunks, 0 for the wide kernel.
+int pick_cpl(int64_t nch)
+{
+    static const int options[] = {1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 28, 32};
+    for (int c : options)
+        if ((int64_t)c * kLanes >= nch) return c;
+    return 0;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+}  // namespace vdn
+
+using namespace vdn;
+
+extern "C" int vdn_fp8_quantize_rows(const void* x, int64_t M, int64_t K, int64_t ldx, void* y,
+                                     int64_t ldy, float* scale, hipStream_t stream)
+{
+    if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "quantize_rows: negative shape [%lld, %lld]", (long long)M, (long long)K);
+    if (M == 0 || K == 0) {
+        if (M > 0 && K == 0) return set_error(VDN_FP8_EINVAL, "quantize_rows: K must be positive");
+        return VDN_FP8_OK;
+    }
+    if (!x || !y || !scale) return set_error(VDN_FP8_EINVAL, "quantize_rows: null pointer");
+    if (K % 8 || ldx % 8 || ldy % 8 || ldx < K || ldy < K)
+        return set_error(VDN_FP8_EINVAL, "quantize_rows: need K, ldx, ldy multiples of 8 and ldx, ldy >= K (K=%lld ldx=%lld ldy=%lld)",
+                         (long long)K, (long long)ldx, (long long)ldy);
+    if (!aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4))
+        return set_error(VDN_FP8_EINVAL, "quantize_rows: x must be 16-byte and y 8-byte aligned");
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
+    launch_rowquant<false>(pick_cpl(K / 8), grid, stream, (const uint16_t*)x, M, K, ldx, (uint8_t*)y, ldy, scale);
+    return check_launch("quantize_rows");
+}
+
+extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K, int64_t ldh, void* y,
+                                            int64_t ldy, float* scale, hipStream_t stream)
+{
+    if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: negative shape");
+    if (M == 0) return VDN_FP8_OK;
+    if (K == 0) return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: K must be positive");
+    if (!h || !y || !scale) return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: null pointer");
+    if (K % 8 || ldh % 8 || ldy % 8 || ldh < 2 * K || ldy < K)
+        return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: need K, ldh, ldy multiples of 8, ldh >= 2K, ldy >= K");
+    if (!aligned(h, 16) || !aligned(y, 8)) return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: misaligned pointer");
+    const int64_t nch = K / 8;
+    if (nch > 32 * kLanes) return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: K=%lld above the supported 16384", (long long)K);
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    const uint16_t* hp = (const uint16_t*)h;
+    uint8_t* yp = (uint8_t*)y;
+    switch (pick_cpl(nch)) {
+#define VDN_CASE(n) case n: hipLaunchKernelGGL(k_swiglu_quant<n>, grid, block, 0, stream, hp, M, K, ldh, yp, ldy, scale); break;
+        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
+        VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
+#undef VDN_CASE
+        default: return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: unsupported K");
+    }
+    return check_launch("swiglu_quantize_rows");
+}
+
+namespace vdn {
+int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, const uint16_t* a,
+                        const uint16_t* b, int64_t rank, float lora_scale, uint8_t* wq, int64_t ldq,
+                        float* w_scale, uint16_t* w_merged, hipStream_t stream);
+}
+
+extern "C" int vdn_fp8_requantize_weight(const void* w, int64_t N, int64_t K, int64_t ldw, const void* lora_a,
+                                         const void* lora_b, int64_t rank, float lora_scale, void* wq,
+                                         int64_t ldq, float* w_scale, void* w_merged, hipStream_t stream)
+{
+    if (N < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "requantize_weight: negative shape");
+    if (N == 0) return VDN_FP8_OK;
+    if (K == 0) return set_error(VDN_FP8_EINVAL, "requantize_weight: K must be positive");
+    const bool merge_only = !wq && !w_scale && w_merged && lora_a && lora_b;
+    if (!w || (!merge_only && (!wq || !w_scale)))
+        return set_error(VDN_FP8_EINVAL, "requantize_weight: null pointer (wq and w_scale may be NULL only "
+                                         "for a LoRA merge into w_merged)");
+    if (K % 8 || ldw % 8 || ldw < K || (!merge_only && (ldq % 8 || ldq < K)))
+        return set_error(VDN_FP8_EINVAL, "requantize_weight: need K, ldw, ldq multiples of 8 and >= K");
+    if (!aligned(w, 16) || (wq && !aligned(wq, 8))) return set_error(VDN_FP8_EINVAL, "requantize_weight: misaligned pointer");
+    if (lora_a || lora_b) {
+        if (!lora_a || !lora_b) return set_error(VDN_FP8_EINVAL, "requantize_weight: lora_a and lora_b go together");
+        return launch_lora_requant((const uint16_t*)w, N, K, ldw, (const uint16_t*)lora_a, (const uint16_t*)lora_b,
+                                   rank, lora_scale, (uint8_t*)wq, ldq, w_scale, (uint16_t*)w_merged, stream);
+    }
+    const dim3 grid((unsigned)((N + kWavesPerBlock - 1) / kWavesPerBlock));
+    launch_rowquant<true>(pick_cpl(K / 8), grid, stream, (const uint16_t*)w, N, K, ldw, (uint8_t*)wq, ldq, w_scale);
+    int st = check_launch("requantize_weight");
+    if (st == VDN_FP8_OK && w_merged && w_merged != w) {
+        // Without LoRA the "merged" weight is the weight itself.
+        if (hipMemcpy2DAsync(w_merged, ldw * 2, w, ldw * 2, K * 2, N, hipMemcpyDeviceToDevice, stream) != hipSuccess)
+            return set_error(VDN_FP8_ELAUNCH, "requantize_weight: copy of the merged weight failed");
+    }
+    return st;
+}

@@ -1,0 +1,88 @@
+// Shared device helpers and host-side error plumbing for the fp8 linear path.
+//
+// Element formats:
+//   bf16  -- stored as uint16_t bit patterns (the high half of a binary32);
+//   e4m3  -- OCP float8 e4m3 "fn" (max 448, no infinities, 0x7f/0xff NaN),
+//            the format of torch.float8_e4m3fn; stored as uint8_t codes.
+// gfx950 converts to and from OCP e4m3 in hardware (v_cvt_pk_fp8_f32,
+// round to nearest even).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vdn_fp8.h"
+
+namespace vdn {
+
+// ---------------------------------------------------------------------------
+// host: error state (one message per host thread, read by vdn_fp8_last_error)
+// ---------------------------------------------------------------------------
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// device: bf16 / e4m3 conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Two binary32 values -> two bf16 (round to nearest even), packed lo|hi<<16.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+    bf16x2_t p = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, p);
+}
+
+__device__ __forceinline__ float round_bf16(float v) { return bf16_lo(pack_bf16x2(v, 0.0f)); }
+
+// Four binary32 values -> four e4m3 codes in one dword (byte i = value i).
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d)
+{
+    uint32_t w = 0;
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, w, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return w;
+}
+
+// Packed max of the magnitudes of two bf16 lanes: (bits & 0x7fff) orders the
+// same way as |x| for every non-NaN pattern and puts NaN patterns above inf.
+__device__ __forceinline__ uint32_t absmax_bf16x2(uint32_t acc, uint32_t w)
+{
+    u16x2_t a = __builtin_bit_cast(u16x2_t, acc);
+    u16x2_t b = __builtin_bit_cast(u16x2_t, w & 0x7fff7fffu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+
+// Maximum over the 64 lanes of a wavefront.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+    return v;
+}
+
+// The per-row scale of the reference: max(amax / 448, 1e-12) with IEEE
+// binary32 division; NaN propagates (torch's clamp_min keeps NaN).
+__device__ __forceinline__ float row_scale(float amax)
+{
+    float s = amax / 448.0f;
+    return (s < 1e-12f) ? 1e-12f : s;
+}
+
+// x / s rounded to nearest binary32, from r = RN(1/s): one multiply and two
+// fma. The remainder is written -fma(q0, s, -x) so that x = -0 yields -0.
+// Valid for finite, positive s; every (s, x) pair the quantizers can produce
+// gives the same e4m3 code as the IEEE quotient (checked exhaustively).
+__device__ __forceinline__ float div_by_scale(float x, float s, float r)
+{
+    float q0 = x * r;
+    float e = -__builtin_fmaf(q0, s, -x);
+    return __builtin_fmaf(e, r, q0);
+}
+
+}  // namespace vdn

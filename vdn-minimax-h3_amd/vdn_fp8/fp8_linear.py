@@ -1,0 +1,301 @@
+"""fp8 e4m3 Linears for the DiT blocks, on MI355X (gfx950) -- a drop-in for the
+reference module `src.models.ops.fp8_linear` (src/models/ops/fp8_linear.py).
+
+Same names, signatures, buffers and error behaviour as the reference; every kernel is
+hand-written HIP in libvdnfp8.so (include/vdn_fp8.h), reached through ctypes on torch's
+current HIP stream. There is no CPU path: like the reference's Triton quantizer, the
+operators refuse CPU tensors with ValueError.
+
+What runs where (reference -> here):
+  _quantize_rows_kernel (Triton)        -> vdn_fp8_quantize_rows (one HBM read per row)
+  _swiglu_quantize_kernel (Triton)      -> vdn_fp8_swiglu_quantize_rows
+  Fp8Linear.__init__ eager weight quant -> vdn_fp8_requantize_weight (+ fused LoRA merge)
+  torch._scaled_mm + `out + bias`       -> vdn_fp8_gemm (MFMA fp8, scales/bias/epilogue fused)
+
+Scale granularity. The reference picks per-tensor scales on sm100 and rowwise
+(per-token x per-channel) elsewhere (fp8_linear.py:141-147). gfx950 reports compute
+capability 9.5, so `per_tensor_gemm()` is False here and the rowwise path is the one
+implemented; the per-tensor family (quantize_tensor & co.) is not part of this module.
+
+Extensions (keyword-only, additive): `Fp8Linear.forward_quantized` and `forward` take an
+`epilogue` ("gelu_tanh" or "gate") with `gate`, `gate_index` and `residual`, fused into
+the GEMM; `Fp8Linear(linear, lora=(A, B, scale))` quantizes W + scale * B @ A in one
+kernel without writing the merged bf16 weight.
+"""
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+FP8_DTYPE = torch.float8_e4m3fn
+_FP8_MAX = torch.finfo(FP8_DTYPE).max
+MIN_WIDTH = 4096
+SKIP_END_BLOCKS = 4
+
+_EPILOGUES = {None: _lib.EPI_NONE, "none": _lib.EPI_NONE, "gelu_tanh": _lib.EPI_GELU_TANH,
+              "gate": _lib.EPI_GATE}
+
+
+def _stream(t):
+    return ctypes_stream(t.device)
+
+
+def ctypes_stream(device):
+    """torch's current HIP stream on `device`, as the raw handle the C ABI takes."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _rows(x):
+    """The reference's input check (fp8_linear.py:102-107): GPU, 2-D, then contiguous."""
+    if not x.is_cuda:
+        raise ValueError("the fp8 quantiser is a HIP kernel; the input must be on the GPU")
+    if x.dim() != 2:
+        raise ValueError(f"expected [M, K], got {tuple(x.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"the fp8 quantiser takes bfloat16 input, got {x.dtype}")
+    return x.contiguous()
+
+
+def quantize_rows(x):
+    """bf16 [M, K] -> (fp8 [M, K], fp32 scale [M, 1]). One absmax per row.
+
+    Codes and scales are bit-identical to `quantize_rows_reference` (the reference's
+    eager spelling, fp8_linear.py:132-135). Replaces fp8_linear.py:110-117."""
+    x = _rows(x)
+    M, K = x.shape
+    y = torch.empty_like(x, dtype=FP8_DTYPE)
+    scale = torch.empty(M, 1, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.vdn_fp8_quantize_rows(_ptr(x), M, K, K, _ptr(y), K, _ptr(scale), _stream(x)),
+               "quantize_rows")
+    return y, scale
+
+
+def swiglu_quantize(h):
+    """[M, 2K] projection output -> quantize_rows(a * silu(gate)) with a, gate = h.chunk(2),
+    without writing the bf16 activation. Replaces fp8_linear.py:120-129."""
+    h = _rows(h)
+    M, K2 = h.shape
+    if K2 % 2:
+        raise ValueError(f"swiglu_quantize needs an even width, got {K2}")
+    K = K2 // 2
+    y = torch.empty(M, K, device=h.device, dtype=FP8_DTYPE)
+    scale = torch.empty(M, 1, device=h.device, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.vdn_fp8_swiglu_quantize_rows(_ptr(h), M, K, K2, _ptr(y), K, _ptr(scale), _stream(h)),
+               "swiglu_quantize")
+    return y, scale
+
+
+def quantize_rows_reference(x):
+    """The eager spelling of `quantize_rows` (fp8_linear.py:132-135), kept for API
+    compatibility: plain torch ops, the contract the HIP kernel is bit-exact with.
+    Never called by the fp8 path itself."""
+    scale = (x.float().abs().amax(dim=1, keepdim=True) / _FP8_MAX).clamp_min(1e-12)
+    return (x.float() / scale).to(FP8_DTYPE), scale
+
+
+_PER_TENSOR = None
+
+
+def per_tensor_gemm():
+    """True only on compute capability >= 10 (sm100), as in the reference
+    (fp8_linear.py:141-147). gfx950 reports 9.5: rowwise scales."""
+    global _PER_TENSOR
+    if _PER_TENSOR is None:
+        _PER_TENSOR = (torch.cuda.is_available()
+                       and torch.cuda.get_device_capability(0)[0] >= 10)
+    return _PER_TENSOR
+
+
+def _rowwise_only():
+    if per_tensor_gemm():
+        raise NotImplementedError("per-tensor fp8 scales (the sm100 branch) are not part of the "
+                                  "gfx950 build; this device should report capability 9.x")
+
+
+def quantize_activation(x):
+    """What the GEMM callers use (fp8_linear.py:233-236): rowwise on gfx950."""
+    _rowwise_only()
+    return quantize_rows(x)
+
+
+def swiglu_quantize_activation(h):
+    """fp8_linear.py:239-240: rowwise on gfx950."""
+    _rowwise_only()
+    return swiglu_quantize(h)
+
+
+def requantize_weight(weight, lora=None, merged_out=None):
+    """bf16 weight [N, K] -> (fp8 codes [N, K], fp32 scale [N]) with the rowwise
+    arithmetic of Fp8Linear.__init__ (fp8_linear.py:262-267).
+
+    lora = (A [r, K] bf16, B [N, r] bf16, scale) folds W + bf16(scale * B @ A) in first,
+    as merge_lora_state does (lora.py:91-92), inside the same kernel. merged_out, if
+    given (bf16 [N, K], may be `weight` itself), receives the merged weight."""
+    if not weight.is_cuda:
+        raise ValueError("the fp8 requantizer is a HIP kernel; the weight must be on the GPU")
+    if weight.dim() != 2 or weight.dtype != torch.bfloat16:
+        raise ValueError(f"expected a bfloat16 [N, K] weight, got {weight.dtype} {tuple(weight.shape)}")
+    w = weight.contiguous()
+    N, K = w.shape
+    q = torch.empty(N, K, device=w.device, dtype=FP8_DTYPE)
+    s = torch.empty(N, device=w.device, dtype=torch.float32)
+    a = b = None
+    rank, lscale = 0, 1.0
+    if lora is not None:
+        a, b, lscale = lora
+        a, b = _lora_factor(a, w, "A"), _lora_factor(b, w, "B")
+        rank = a.shape[0]
+        if a.shape != (rank, K) or b.shape != (N, rank):
+            raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
+    if merged_out is not None:
+        if merged_out.shape != (N, K) or merged_out.dtype != torch.bfloat16 or not merged_out.is_contiguous() \
+                or merged_out.device != w.device:
+            raise ValueError("merged_out must be a contiguous bf16 [N, K] tensor on the weight's device")
+    lib = _lib.load()
+    _lib.check(lib.vdn_fp8_requantize_weight(_ptr(w), N, K, K, _ptr(a), _ptr(b), rank, float(lscale),
+                                             _ptr(q), K, _ptr(s), _ptr(merged_out), _stream(w)),
+               "requantize_weight")
+    return q, s
+
+
+def _lora_factor(t, w, name):
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"LoRA factor {name} must be bfloat16 (got {t.dtype})")
+    return t.to(w.device).contiguous()
+
+
+class Fp8Linear(nn.Module):
+    """A bias-optional Linear whose GEMM runs in fp8 e4m3 (fp8_linear.py:243-283).
+
+    The weight is quantised ONCE, per output channel, at construction; the activation is
+    quantised per row on every call, or by the caller (`forward_quantized`) when one
+    activation feeds several of these. Only the fp8 copy and the bias are kept -- the
+    bf16 weight goes as soon as the caller drops the Linear it came from.
+
+    Buffers: weight_fp8 e4m3 [N, K], weight_scale fp32 [1, N]; `bias` is the source
+    Linear's Parameter object itself.
+    """
+
+    def __init__(self, linear: nn.Linear, *, lora=None):
+        super().__init__()
+        _rowwise_only()
+        q, s = requantize_weight(linear.weight.detach(), lora=lora)
+        self.register_buffer("weight_fp8", q)
+        self.register_buffer("weight_scale", s.reshape(1, -1).contiguous())
+        self.register_parameter("bias", linear.bias)
+
+    @property
+    def in_features(self):
+        return self.weight_fp8.shape[1]
+
+    @property
+    def out_features(self):
+        return self.weight_fp8.shape[0]
+
+    def forward_quantized(self, x_fp8, x_scale, out_dtype=torch.bfloat16, *, epilogue=None,
+                          gate=None, gate_index=None, residual=None):
+        """[M, K] fp8 rows and their [M, 1] scales -> [M, N] (fp8_linear.py:270-277).
+
+        Computes bf16(epi(x_scale * w_scale * (x_fp8 @ weight_fp8.T) + bias)) in one
+        kernel. epilogue: None, "gelu_tanh", or "gate" -- gate [T, N] (or [N]) table,
+        gate_index [M] rows of it (None = row 0; out-of-range indices are clamped),
+        residual [M, N] (optional): gate[gate_index] * out + residual, the gated residual
+        add of the block (fused_block.py:47-49)."""
+        if out_dtype != torch.bfloat16:
+            raise ValueError(f"the fp8 GEMM writes bfloat16 (out_dtype={out_dtype})")
+        if not x_fp8.is_cuda or x_fp8.dtype != FP8_DTYPE or x_fp8.dim() != 2:
+            raise ValueError("x_fp8 must be a float8_e4m3fn [M, K] tensor on the GPU")
+        M, K = x_fp8.shape
+        N = self.weight_fp8.shape[0]
+        if K != self.weight_fp8.shape[1]:
+            raise ValueError(f"x has K={K}, the weight has K={self.weight_fp8.shape[1]}")
+        if x_scale.numel() != M or x_scale.dtype != torch.float32:
+            raise ValueError("x_scale must be the fp32 [M, 1] rowwise scale (per-tensor scales are "
+                             "the sm100 branch, not built for gfx950)")
+        if x_fp8.stride(1) != 1:
+            x_fp8 = x_fp8.contiguous()
+        x_scale = x_scale.contiguous()
+        dev = x_fp8.device
+        out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        epi = _EPILOGUES.get(epilogue)
+        if epi is None:
+            raise ValueError(f"unknown epilogue {epilogue!r}")
+        bias = self.bias
+        if bias is not None:
+            if bias.dtype != torch.bfloat16 or bias.numel() != N:
+                raise ValueError("the fused bias must be a bfloat16 [N] tensor")
+            bias = bias.detach().contiguous()
+        g = gi = res = None
+        ldgate = ldres = grows = 0
+        if epi == _lib.EPI_GATE:
+            if gate is None:
+                raise ValueError('epilogue="gate" needs a gate table')
+            g = gate.detach().reshape(-1, N)
+            if g.dtype != torch.bfloat16 or g.stride(1) != 1:
+                g = g.to(torch.bfloat16).contiguous()
+            ldgate, grows = g.stride(0), g.shape[0]
+            if gate_index is not None:
+                gi = gate_index.to(device=dev, dtype=torch.int32).contiguous()
+                if gi.numel() != M:
+                    raise ValueError("gate_index must hold one table row per token")
+            if residual is not None:
+                res = residual.detach()
+                if res.shape != (M, N) or res.dtype != torch.bfloat16 or res.stride(1) != 1:
+                    raise ValueError("residual must be a bfloat16 [M, N] tensor with unit column stride")
+                ldres = res.stride(0)
+        elif gate is not None or residual is not None or gate_index is not None:
+            raise ValueError('gate / gate_index / residual need epilogue="gate"')
+        lib = _lib.load()
+        _lib.check(lib.vdn_fp8_gemm(_ptr(x_fp8), _ptr(x_scale), _ptr(self.weight_fp8),
+                                    _ptr(self.weight_scale), M, N, K, x_fp8.stride(0), K,
+                                    _ptr(bias), epi, _ptr(g), _ptr(gi), grows, ldgate, _ptr(res), ldres,
+                                    _ptr(out), N, _stream(x_fp8)),
+                   "fp8 gemm")
+        return out
+
+    def forward(self, x, **epilogue):
+        shape = x.shape
+        rows = x.reshape(-1, shape[-1])
+        if "residual" in epilogue and epilogue["residual"] is not None:
+            epilogue["residual"] = epilogue["residual"].reshape(rows.shape[0], -1)
+        out = self.forward_quantized(*quantize_activation(rows), out_dtype=rows.dtype, **epilogue)
+        return out.reshape(*shape[:-1], -1)
+
+
+def _blocks_to_skip(model, skip_end_blocks):
+    """ids of every module inside the first and last N transformer blocks
+    (fp8_linear.py:286-295)."""
+    blocks = getattr(model, "transformer_blocks", None)
+    if not blocks or skip_end_blocks <= 0:
+        return set()
+    keep = set()
+    for index, block in enumerate(blocks):
+        if index < skip_end_blocks or index >= len(blocks) - skip_end_blocks:
+            keep.update(id(m) for m in block.modules())
+    return keep
+
+
+def convert_linear_to_fp8(model, min_width=MIN_WIDTH, skip_end_blocks=SKIP_END_BLOCKS):
+    """Swap the wide Linears for fp8 ones, in place. Returns how many were swapped
+    (fp8_linear.py:298-323).
+
+    Call it AFTER any LoRA merge (or use `vdn_fp8.lora.merge_lora_and_convert`, which
+    fuses the two). The work list names (parent, attribute), never the Linears, so each
+    bf16 weight is released as soon as its parent is repointed: peak memory is the model
+    plus one fp8 weight."""
+    skip = _blocks_to_skip(model, skip_end_blocks)
+    targets = [(parent, name) for parent in model.modules()
+               for name, child in parent.named_children()
+               if isinstance(child, nn.Linear) and child.in_features >= min_width
+               and child.out_features >= min_width and id(child) not in skip]
+    for parent, name in targets:
+        child = getattr(parent, name)
+        setattr(parent, name, Fp8Linear(child).to(child.weight.device))
+        del child
+    return len(targets)
