@@ -93,10 +93,10 @@ __device__ __forceinline__ void tile_coords(int b, int tiles_m, int tiles_n, int
 }
 
 // Epilogue for 4 consecutive output channels n .. n+3 of token m: the
-// reference's rounding points, then one 8-byte store.
+// reference's rounding points; returns the 4 bf16 results packed.
 template <int EPI>
-__device__ __forceinline__ void store4(const GemmArgs& p, int64_t m, int64_t n, const float* acc, float sxm,
-                                       const uint16_t* grow)
+__device__ __forceinline__ uint2 epi4(const GemmArgs& p, int64_t m, int64_t n, const float* acc, float sxm,
+                                      const uint16_t* grow)
 {
     const float4 sw = *reinterpret_cast<const float4*>(p.sw + n);
     const float swv[4] = {sw.x, sw.y, sw.z, sw.w};
@@ -122,7 +122,14 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int64_t m, int64_t n, 
             v[0] += bf16_lo(rv.x); v[1] += bf16_hi(rv.x); v[2] += bf16_lo(rv.y); v[3] += bf16_hi(rv.y);
         }
     }
-    *reinterpret_cast<uint2*>(p.out + m * p.ldo + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+template <int EPI>
+__device__ __forceinline__ void store4(const GemmArgs& p, int64_t m, int64_t n, const float* acc, float sxm,
+                                       const uint16_t* grow)
+{
+    *reinterpret_cast<uint2*>(p.out + m * p.ldo + n) = epi4<EPI>(p, m, n, acc, sxm, grow);
 }
 
 template <int EPI>
@@ -175,6 +182,19 @@ __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
 constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | (0 << 8) | ((vm >> 4) << 14); }
 
+// This wave's copies, except the VM most recent, have landed and its LDS reads
+// are done; then all waves meet. The scheduling barriers keep the compiler from
+// moving instructions across (MFMAs touch no memory and would otherwise float).
+template <int VM>
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VM));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------------------
 // main kernel: K % 128 == 0
 // ---------------------------------------------------------------------------
@@ -182,6 +202,7 @@ namespace mainloop {
 constexpr int BK = 128;                     // K bytes per block (one LDS stage)
 constexpr int kStage = (BM + BN) * BK;      // 64 KiB: X tile, then W tile
 constexpr int kCopies = BM * BK / 1024 / 4; // 1 KiB copies per wave per tile per block (8)
+constexpr int kNoVmWait = 63;               // s_waitcnt vmcnt field maximum: no condition
 
 // Row r, 16-byte chunk c (0..7) of a tile sits at chunk c ^ ((r >> 1) & 7) of
 // its 128-byte LDS row.
@@ -217,102 +238,146 @@ void k_gemm_fp8(GemmArgs p)
         woff[i] = (uint32_t)(r * p.ldw) + c * 16;
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
-    // Copies of block j into stage j % 2. Blocks past the end still issue
-    // their copies with an out-of-range offset (the buffer returns zeros and no
-    // memory is read), keeping the loop free of data-dependent branches.
-    auto issue = [&](int j) {
-        const uint32_t st = lds_base + (uint32_t)(j & 1) * kStage;
-        const uint32_t kb = (uint32_t)j * BK;
-        const bool live = j < nk;
-#pragma unroll
-        for (int i = 0; i < kCopies; ++i) {
-            copy16_to_lds(xr, st + (64 * wave + 8 * i) * BK, live ? xoff[i] : 0x80000000u, kb);
-            copy16_to_lds(wr, st + BM * BK + (64 * wave + 8 * i) * BK, live ? woff[i] : 0x80000000u, kb);
-        }
-    };
-
+    // Blocks past the end still issue their copies, with an out-of-range
+    // offset (the buffer returns zeros and no memory is read), so the loop has
+    // no data-dependent branches and the vmcnt bookkeeping stays fixed.
     // Fragments of half h (k bytes 64 h .. 64 h + 63) of block j: lane reads row
     // (base + lane % 32), k bytes 64 h + 32 (lane / 32) .. +31, as two 16-byte chunks.
+    // Fragment f < 4 is W rows wn*128 + 32 f.., f >= 4 is X rows wm*128 + 32 (f-4)..
     const int frow = lane & 31, fh = lane >> 5;
-    auto read_frag = [&](const uint8_t* s, int row, int h) -> i32x8_t {
+    auto read_frag = [&](int j, int h, int f) -> i32x8_t {
+        const uint8_t* st = smem + (j & 1) * kStage;
+        const uint8_t* s = f < 4 ? st + BM * BK : st;
+        const int row = (f < 4 ? wn * 128 + 32 * f : wm * 128 + 32 * (f - 4)) + frow;
         const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh));
         const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh + 1));
         return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     };
-    auto read_half = [&](int j, int h, i32x8_t* wf, i32x8_t* xf) {
-        const uint8_t* st = smem + (j & 1) * kStage;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) wf[t] = read_frag(st + BM * BK, wn * 128 + 32 * t + frow, h);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) xf[u] = read_frag(st, wm * 128 + 32 * u + frow, h);
+    // Copy c (0..15) of block j: c < 8 is X rows 64 wave + 8 c .., else W rows.
+    auto copy = [&](int j, int c) {
+        const uint32_t st = lds_base + (uint32_t)(j & 1) * kStage;
+        const uint32_t kb = (uint32_t)j * BK;
+        const bool live = j < nk;
+        const int i = c & 7;
+        if (c < 8) copy16_to_lds(xr, st + (64 * wave + 8 * i) * BK, live ? xoff[i] : 0x80000000u, kb);
+        else copy16_to_lds(wr, st + BM * BK + (64 * wave + 8 * i) * BK, live ? woff[i] : 0x80000000u, kb);
     };
 
     f32x16_t acc[4][4] = {};
-    auto mfmas = [&](const i32x8_t* wf, const i32x8_t* xf) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                acc[t][u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t], xf[u], acc[t][u], 0, 0, 0, 0, 0, 0);
+    // MFMA q (0..15) of a half-step: acc[t][u] += W frag t x X frag u, t = q % 4, u = q / 4.
+    auto mfma = [&](const i32x8_t* wf, const i32x8_t* xf, int q) {
+        const int t = q & 3, u = q >> 2;
+        acc[t][u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t], xf[u], acc[t][u], 0, 0, 0, 0, 0, 0);
     };
+    auto read_into = [&](int j, int h, int f, i32x8_t* wf, i32x8_t* xf) {
+        if (f < 4) wf[f] = read_frag(j, h, f);
+        else xf[f - 4] = read_frag(j, h, f);
+    };
+    auto fence = [&]() { __builtin_amdgcn_sched_barrier(0); };
 
     // Prologue: blocks 0 and 1 in flight; wait for block 0, read its first half.
     // The s_nop keeps 5 wait states between the v_readfirstlane writes of the
     // descriptors and their first use by a buffer load (an SGPR hazard that the
     // compiler does not see through inline assembly).
     asm volatile("s_nop 4");
-    issue(0);
-    issue(1);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * kCopies));
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < 2 * kCopies; ++c) copy(0, c);
+#pragma unroll
+    for (int c = 0; c < 2 * kCopies; ++c) copy(1, c);
+    wave_sync<2 * kCopies>();
     i32x8_t w0[4], x0[4], w1[4], x1[4];
-    read_half(0, 0, w0, x0);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) read_into(0, 0, f, w0, x0);
 
-    // One trip per block j, two MFMA half-steps:
-    //  half 0: read half 1 of block j into set 1 while the MFMAs use set 0;
-    //  half 1: wait for block j+1 (and for this wave's reads of block j), meet
-    //          the other waves, refill stage j % 2 with block j+2, read half 0
-    //          of block j+1 into set 0 while the MFMAs use set 1.
-    // Block j+2's copies have two half-steps (32 MFMAs) to land. The scheduling
-    // groups put each half-step's 16 LDS reads ahead of its 16 MFMAs.
+    // One trip per block j, two half-steps of 16 MFMAs. With one wavefront per
+    // SIMD every stalled issue idles the matrix core, so each MFMA is followed
+    // by at most one copy and two fragment reads, in a fixed order:
+    //   half 0 (set 0): MFMAs 0-3 each read 2 fragments of block j half 1 into
+    //     set 1; after MFMA 7, barrier A (this wave's reads done, then all
+    //     waves): stage j % 2 is free; MFMAs 8-15 each issue one X copy of
+    //     block j+2 into it.
+    //   barrier B: this wave's copies of block j+1 have landed (only the 8
+    //     copies just issued may be pending), then all waves.
+    //   half 1 (set 1): MFMAs 0-7 each issue one W copy of block j+2; MFMAs 0-3
+    //     also read 2 fragments of block j+1 half 0 into set 0.
+    // A block's copies thus have 1.5 to 2 half-step pairs to land.
     for (int j = 0; j < nk; ++j) {
-        read_half(j, 1, w1, x1);
-        mfmas(w0, x0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        issue(j + 2);
-        read_half(j + 1, 0, w0, x0);
-        mfmas(w1, x1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            mfma(w0, x0, q);
+            fence();
+            if (q < 4) {
+                read_into(j, 1, 2 * q, w1, x1);
+                read_into(j, 1, 2 * q + 1, w1, x1);
+            }
+            if (q == 7) wave_sync<kNoVmWait>();
+            if (q >= 8) copy(j + 2, q - 8);
+            fence();
+        }
+        wave_sync<kCopies>();
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            mfma(w1, x1, q);
+            fence();
+            if (q < 8) copy(j + 2, 8 + q);
+            if (q < 4) {
+                read_into(j + 1, 0, 2 * q, w0, x0);
+                read_into(j + 1, 0, 2 * q + 1, w0, x0);
+            }
+            fence();
+        }
     }
     // No copy may still be writing LDS when the workgroup ends.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 
-    // Epilogue: acc[t][u][r] is n = n0 + wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4,
-    // m = m0 + wm*128 + 32 u + lane%32.
+    // Epilogue. acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4,
+    // m = wm*128 + 32 u + lane%32 (tile-relative). The results are finished in
+    // that layout (4 consecutive n per lane), staged through LDS -- free now --
+    // and written back as 16-byte pieces of whole 256-byte row segments: lane L
+    // of a store covers row 4 i + L/16, channels 8 (L%16) .. +7.
+    // Each wave stages its 128 x 128 quadrant (32 KiB) in its own LDS region,
+    // rows of 256 bytes; the 16-byte chunk c of row m sits at c ^ (m & 15) and its
+    // two 8-byte halves are swapped when (m >> 4) & 1 -- every 32-lane write
+    // then hits 32 distinct 8-byte bank pairs.
+    __builtin_amdgcn_s_barrier();          // every wave is done with the stages
+    asm volatile("" ::: "memory");
+    uint8_t* const tile_lds = smem + wave * 32768;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int64_t m = m0 + wm * 128 + 32 * u + frow;
-        if (m >= p.M) continue;
+        const int ml = 32 * u + frow;
+        const int64_t m = min(m0 + wm * 128 + ml, p.M - 1);   // rows past M: computed, never stored
         const float sxm = p.sx[m];
         const uint16_t* grow = gate_row<EPI>(p, m);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t n = n0 + wn * 128 + 32 * t + 8 * q + 4 * fh;
-                if (n >= p.N) continue;
+                const int nl = 32 * t + 8 * q + 4 * fh;
+                const int64_t n = min(n0 + wn * 128 + nl, p.N - 4);
                 const float a4[4] = {acc[t][u][4 * q], acc[t][u][4 * q + 1], acc[t][u][4 * q + 2], acc[t][u][4 * q + 3]};
-                store4<EPI>(p, m, n, a4, sxm, grow);
+                const uint2 v = epi4<EPI>(p, m, n, a4, sxm, grow);
+                const int c = nl >> 3, half = ((nl >> 2) & 1) ^ ((ml >> 4) & 1);
+                *reinterpret_cast<uint2*>(tile_lds + ml * 256 + ((c ^ (ml & 15)) << 4) + (half << 3)) = v;
             }
+    }
+    const int64_t mq = m0 + wm * 128, nq = n0 + wn * 128;
+    const int rc = lane & 15;                          // 16-byte chunk of the row this lane stores
+    const int64_t n = nq + 8 * rc;
+    const bool vec16 = ((p.ldo & 7) == 0) && (((uintptr_t)p.out & 15) == 0);
+#pragma unroll 4
+    for (int i = 0; i < 32; ++i) {
+        const int ml = 4 * i + (lane >> 4);
+        uint4 v = *reinterpret_cast<const uint4*>(tile_lds + ml * 256 + ((rc ^ (ml & 15)) << 4));
+        if ((ml >> 4) & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        const int64_t m = mq + ml;
+        if (m >= p.M || n >= p.N) continue;
+        uint16_t* dst = p.out + m * p.ldo + n;
+        if (vec16 && n + 8 <= p.N) {
+            *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+            if (n + 8 <= p.N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+        }
     }
 }
 
