@@ -108,7 +108,8 @@ int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
  *           reference function; the gate epilogue replaces _post_ref /
  *           the compiled `post`, src/models/ops/fused_block.py:47-49,101-110.
  * Requires: K % 16 == 0; ldx, ldw % 16 == 0; ldo, ldres, ldgate % 4 == 0;
- *           xq, wq 16-byte aligned; out, residual, gate, bias 8-byte aligned.
+ *           xq, wq, x_scale, w_scale, bias, gate_index 16-byte aligned;
+ *           out, residual, gate 8-byte aligned.
  */
 int vdn_fp8_gemm(const void *xq, const float *x_scale, const void *wq, const float *w_scale,
                  int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,

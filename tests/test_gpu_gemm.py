@@ -59,6 +59,8 @@ def _check(x_bits, w_bits, b_bits, device, rows=None, **epi):
     res = epi.get("residual")
     gi = epi.get("gate_index")
     args = (qxn, sxn, codes(f.weight_fp8), f.weight_scale.cpu().numpy().reshape(-1))
+    if gi is not None:                         # the ABI clamps indices into the table
+        gi = np.clip(gi, 0, (epi["gate"].shape[0] if epi["gate"].ndim == 2 else 1) - 1)
     kw = dict(bias=b_bits, epilogue=epi.get("epilogue") or "none", gate=epi.get("gate"),
               gate_index=None if gi is None else gi[sel], residual=None if res is None else res[sel])
     want = O.dequant_linear(*args, **kw)
@@ -133,6 +135,25 @@ def test_gemm_gate_broadcast(device):
     M, N, K = 257, 512, 512
     gate = O.bf16_encode(rng.uniform(0, 2, N).astype(np.float32))
     _check(_rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.02), None, device, epilogue="gate", gate=gate)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4352, 128), (4352, 4096, 384), (4100, 4356, 256)])
+def test_gemm_many_tiles(device, M, N, K):
+    """More 256 x 256 tiles than compute units: each workgroup walks several tiles,
+    the copy stream running across tile boundaries (K = 128: one block per tile)."""
+    print(f"gemm M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    _check(_rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.05), _rand(rng, (N,), 0.1), device)
+
+
+def test_gemm_many_tiles_gate(device):
+    rng = np.random.default_rng(12)
+    M, N, K, T = 4352, 4100, 256, 5
+    gate = O.bf16_encode(rng.uniform(-2, 2, (T, N)).astype(np.float32))
+    gi = rng.integers(-1, T + 1, M).astype(np.int32)           # out-of-range rows clamp
+    res = _rand(rng, (M, N), 1.0)
+    _check(_rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.05), _rand(rng, (N,), 0.1), device,
+           epilogue="gate", gate=gate, gate_index=gi, residual=res)
 
 
 def test_gemm_single_workload(device):

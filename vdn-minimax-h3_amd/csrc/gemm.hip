@@ -38,6 +38,9 @@
 // whose last step is filled through VGPRs with zeros past K.
 #include <stdint.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "vdn_common.h"
 
 namespace vdn {
@@ -196,39 +199,71 @@ __device__ __forceinline__ void wave_sync()
 }
 
 // ---------------------------------------------------------------------------
-// main kernel: K % 128 == 0
+// main kernel: K % 128 == 0, persistent
 // ---------------------------------------------------------------------------
 namespace mainloop {
 constexpr int BK = 128;                     // K bytes per block (one LDS stage)
 constexpr int kStage = (BM + BN) * BK;      // 64 KiB: X tile, then W tile
 constexpr int kCopies = BM * BK / 1024 / 4; // 1 KiB copies per wave per tile per block (8)
+constexpr int kBlockCopies = 2 * kCopies;   // X and W: 16 per wave per block
 constexpr int kNoVmWait = 63;               // s_waitcnt vmcnt field maximum: no condition
+constexpr int kScal = 2 * kStage;           // per-tile vectors, two buffers of 4 x 1 KiB
+constexpr int kStgRow = 144;                // epilogue staging row: 128 bytes + 16 of padding
+constexpr int kStgWave = 32 * kStgRow;      // 32 rows per wave
+constexpr int kStg = kScal + 8192;          // epilogue staging
+constexpr int kLds = kStg + 4 * kStgWave;   // 154 KiB
+constexpr int kEpiStores = 32;              // 16-byte stores per wave per tile (fast epilogue)
 
 // Row r, 16-byte chunk c (0..7) of a tile sits at chunk c ^ ((r >> 1) & 7) of
 // its 128-byte LDS row.
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 }  // namespace mainloop
 
-template <int EPI>
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
+{
+    const uint64_t a = (uint64_t)base;
+    bytes = max(min(bytes, (int64_t)0x7fffffff), (int64_t)0);
+    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu)),
+                   __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), kRsrcWord3};
+}
+
+// One workgroup per CU walks tiles blockIdx.x, + gridDim.x, ... The copies form
+// one stream of 128-byte K blocks across those tiles, so the next tile's first
+// two blocks are in flight while this tile's epilogue runs. Per block g (stage
+// g % 2), two half-steps of 16 MFMAs:
+//   half 0: MFMAs 0-3 read the half-1 fragments of g; barrier A after MFMA 7
+//     (stage g % 2 is then free); MFMAs 8-15 issue the X copies of block g+2.
+//   half 1: MFMAs 0-7 issue the W copies of block g+2; barrier B after MFMA 7:
+//     this wave's copies of block g+1 have landed (newer ones may be pending),
+//     then all waves; MFMAs 8-15 read the half-0 fragments of g+1.
+// A tile's vectors (w_scale, x_scale, bias, gate rows) are copied into one of
+// two scalar buffers at the start of the tile before, one copy per wave. The
+// epilogue stages through LDS of its own.
+//
+// FAST (no gate epilogue, 16-byte aligned output rows): the epilogue issues
+// exactly kEpiStores buffer stores per wave, columns past N sent out of range
+// (dropped), so the waits that follow count them and the stores drain while
+// the next tile runs. Otherwise the waits also cover the epilogue's memory
+// operations.
+template <int EPI, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm_fp8(GemmArgs p)
 {
     using namespace mainloop;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+    constexpr int kE = FAST ? kEpiStores : 0;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
-    int tm, tn;
-    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int T = p.tiles_m * p.tiles_n;
     const int nk = (int)(p.K / BK);
+    const int stride = gridDim.x;
 
     // Copies: this wave fills rows 64 wave .. 64 wave + 63 of each tile, 8 rows
     // (1 KiB) per copy. Lane L lands at row +L/8, physical chunk L%8, so it
     // fetches logical chunk (L%8) ^ ((row >> 1) & 7), row = 64 wave + 8 i + L/8.
-    const i32x4_t xr = tile_rsrc_words(p.xq + m0 * p.ldx, p.M - m0, p.ldx);
-    const i32x4_t wr = tile_rsrc_words(p.wq + n0 * p.ldw, p.N - n0, p.ldw);
     uint32_t xoff[kCopies], woff[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
@@ -238,147 +273,279 @@ void k_gemm_fp8(GemmArgs p)
         woff[i] = (uint32_t)(r * p.ldw) + c * 16;
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
-    // Blocks past the end still issue their copies, with an out-of-range
-    // offset (the buffer returns zeros and no memory is read), so the loop has
-    // no data-dependent branches and the vmcnt bookkeeping stays fixed.
-    // Fragments of half h (k bytes 64 h .. 64 h + 63) of block j: lane reads row
-    // (base + lane % 32), k bytes 64 h + 32 (lane / 32) .. +31, as two 16-byte chunks.
-    // Fragment f < 4 is W rows wn*128 + 32 f.., f >= 4 is X rows wm*128 + 32 (f-4)..
+
+    // Producer: the next block to copy is block pj of tile ptile. Blocks of
+    // tiles past the end still issue their copies, through empty descriptors
+    // (zeros, no memory read), so the vmcnt bookkeeping stays fixed.
+    int ptile = blockIdx.x, pj = 0;
+    i32x4_t xr, wr;
+    auto producer_tile = [&]() {
+        int64_t xb = 0, wb = 0;
+        const uint8_t* xa = p.xq;
+        const uint8_t* wa = p.wq;
+        if (ptile < T) {
+            int tm, tn;
+            tile_coords(ptile, p.tiles_m, p.tiles_n, tm, tn);
+            const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+            xa += m0 * p.ldx;
+            wa += n0 * p.ldw;
+            xb = min(p.M - m0, (int64_t)BM) * p.ldx;
+            wb = min(p.N - n0, (int64_t)BN) * p.ldw;
+        }
+        xr = rsrc_words(xa, xb);
+        wr = rsrc_words(wa, wb);
+        asm volatile("s_nop 4");   // SGPR write by VALU -> use as a buffer descriptor
+    };
+    // Copy c (0..15) of the producer's block into stage st: c < 8 is X rows
+    // 64 wave + 8 c .., else W rows.
+    auto copy = [&](int st, int c) {
+        const uint32_t dst = lds_base + (uint32_t)st * kStage;
+        const uint32_t kb = (uint32_t)pj * BK;
+        const int i = c & 7;
+        if (c < 8) copy16_to_lds(xr, dst + (64 * wave + 8 * i) * BK, xoff[i], kb);
+        else copy16_to_lds(wr, dst + BM * BK + (64 * wave + 8 * i) * BK, woff[i], kb);
+    };
+    auto advance = [&]() {
+        if (++pj == nk) {
+            pj = 0;
+            ptile += stride;
+            producer_tile();
+        }
+    };
+    // The vectors of the k-th tile of this workgroup go to scalar buffer k % 2:
+    // wave 0 w_scale[n0 ..+255], wave 1 x_scale[m0 ..+255], wave 2 bias[n0 ..+511]
+    // (256 used), wave 3 gate_index[m0 ..+255]. Missing ones read as zeros.
+    auto scal_copy = [&](int t, int buf) {
+        const void* base = p.sx;
+        int64_t bytes = 0;
+        if (t < T) {
+            int tm, tn;
+            tile_coords(t, p.tiles_m, p.tiles_n, tm, tn);
+            const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+            if (wave == 0) { base = p.sw + n0; bytes = min(p.N - n0, (int64_t)256) * 4; }
+            else if (wave == 1) { base = p.sx + m0; bytes = min(p.M - m0, (int64_t)256) * 4; }
+            else if (wave == 2) { if (p.bias) { base = p.bias + n0; bytes = min(p.N - n0, (int64_t)512) * 2; } }
+            else if (p.gate_index) { base = p.gate_index + m0; bytes = min(p.M - m0, (int64_t)256) * 4; }
+        }
+        const i32x4_t r = rsrc_words(base, bytes);
+        asm volatile("s_nop 4");
+        // the lane index recomputed here rather than kept live across the K loop
+        uint32_t zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        const uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero;
+        copy16_to_lds(r, lds_base + kScal + buf * 4096 + wave * 1024, l * 16, 0);
+    };
+
+    // Fragments of half h (k bytes 64 h .. 64 h + 63) of the block in stage st:
+    // lane reads row (base + lane % 32), k bytes 64 h + 32 (lane / 32) .. +31, as
+    // two 16-byte chunks. Fragment f < 4 is W rows wn*128 + 32 f.., f >= 4 is X
+    // rows wm*128 + 32 (f-4)..
     const int frow = lane & 31, fh = lane >> 5;
-    auto read_frag = [&](int j, int h, int f) -> i32x8_t {
-        const uint8_t* st = smem + (j & 1) * kStage;
-        const uint8_t* s = f < 4 ? st + BM * BK : st;
+    auto read_frag = [&](int st, int h, int f) -> i32x8_t {
+        const uint8_t* s = smem + st * kStage + (f < 4 ? BM * BK : 0);
         const int row = (f < 4 ? wn * 128 + 32 * f : wm * 128 + 32 * (f - 4)) + frow;
         const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh));
         const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh + 1));
         return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     };
-    // Copy c (0..15) of block j: c < 8 is X rows 64 wave + 8 c .., else W rows.
-    auto copy = [&](int j, int c) {
-        const uint32_t st = lds_base + (uint32_t)(j & 1) * kStage;
-        const uint32_t kb = (uint32_t)j * BK;
-        const bool live = j < nk;
-        const int i = c & 7;
-        if (c < 8) copy16_to_lds(xr, st + (64 * wave + 8 * i) * BK, live ? xoff[i] : 0x80000000u, kb);
-        else copy16_to_lds(wr, st + BM * BK + (64 * wave + 8 * i) * BK, live ? woff[i] : 0x80000000u, kb);
-    };
-
-    f32x16_t acc[4][4] = {};
+    f32x16_t acc[4][4];
     // MFMA q (0..15) of a half-step: acc[t][u] += W frag t x X frag u, t = q % 4, u = q / 4.
     auto mfma = [&](const i32x8_t* wf, const i32x8_t* xf, int q) {
         const int t = q & 3, u = q >> 2;
         acc[t][u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t], xf[u], acc[t][u], 0, 0, 0, 0, 0, 0);
     };
-    auto read_into = [&](int j, int h, int f, i32x8_t* wf, i32x8_t* xf) {
-        if (f < 4) wf[f] = read_frag(j, h, f);
-        else xf[f - 4] = read_frag(j, h, f);
+    auto read_into = [&](int st, int h, int f, i32x8_t* wf, i32x8_t* xf) {
+        if (f < 4) wf[f] = read_frag(st, h, f);
+        else xf[f - 4] = read_frag(st, h, f);
     };
     auto fence = [&]() { __builtin_amdgcn_sched_barrier(0); };
 
-    // Prologue: blocks 0 and 1 in flight; wait for block 0, read its first half.
-    // The s_nop keeps 5 wait states between the v_readfirstlane writes of the
-    // descriptors and their first use by a buffer load (an SGPR hazard that the
-    // compiler does not see through inline assembly).
-    asm volatile("s_nop 4");
+    // Epilogue of the tile at (m0, n0) with its vectors in scalar buffer sb.
+    // acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4, m = wm*128 +
+    // 32 u + lane%32 (tile-relative). Per u and per 64-column half th the wave
+    // finishes its 32 x 64 slab in that layout (4 consecutive n per lane),
+    // writes it to its staging (32 rows of 128 bytes, padded to 144), reads it
+    // back by rows and stores 16-byte pieces of whole 128-byte row segments: lane
+    // L covers row 8 i + L/8, channels 8 (L%8) .. +7. The gate and residual
+    // apply in that row layout.
+    const bool gate16 = ((p.ldgate & 7) == 0) && (((uintptr_t)p.gate & 15) == 0);
+    const bool res16 = ((p.ldres & 7) == 0) && (((uintptr_t)p.residual & 15) == 0);
+    auto epilogue = [&](int64_t m0, int64_t n0, int sb) {
+        // Every lane-dependent value here derives from an opaque zero, so the
+        // compiler recomputes it per tile instead of holding it in registers
+        // across the K loop.
+        uint32_t zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        const int el = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
+        const int frow = el & 31, fh = el >> 5, cc = el & 7, rl = el >> 3;
+        const uint8_t* scal = smem + kScal + sb * 4096;
+        const float* s_sw = reinterpret_cast<const float*>(scal);
+        const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
+        const uint16_t* s_bias = reinterpret_cast<const uint16_t*>(scal + 2048);
+        const int32_t* s_gi = reinterpret_cast<const int32_t*>(scal + 3072);
+        uint8_t* const stg = smem + kStg + wave * kStgWave;
+        const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.out + m0 * p.ldo), 0, (int)min(min(p.M - m0, (int64_t)BM) * p.ldo * 2, (int64_t)0x7fffffff), kRsrcWord3);
+        const uint32_t ldo2 = (uint32_t)p.ldo * 2;
 #pragma unroll
-    for (int c = 0; c < 2 * kCopies; ++c) copy(0, c);
+        for (int uu = 0; uu < 4; ++uu) {
+            const int u = 3 - uu;
+            const float sxm = s_sx[wm * 128 + 32 * u + frow];
 #pragma unroll
-    for (int c = 0; c < 2 * kCopies; ++c) copy(1, c);
-    wave_sync<2 * kCopies>();
+            for (int tt = 0; tt < 2; ++tt) {
+                const int th = 1 - tt;
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int t = 2 * th + t2;
+                        const int nl = wn * 128 + 32 * t + 8 * q + 4 * fh;
+                        const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
+                        const float swv[4] = {sw.x, sw.y, sw.z, sw.w};
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = round_bf16(acc[t][u][4 * q + e] * (sxm * swv[e]));
+                        if (p.bias) {
+                            const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
+                            v[0] = round_bf16(v[0] + bf16_lo(b.x)); v[1] = round_bf16(v[1] + bf16_hi(b.x));
+                            v[2] = round_bf16(v[2] + bf16_lo(b.y)); v[3] = round_bf16(v[3] + bf16_hi(b.y));
+                        }
+                        if (EPI == VDN_FP8_EPI_GELU_TANH) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+                        }
+                        *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) =
+                            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    }
+                // these accumulators start the next tile from zero
+                acc[2 * th][u] = f32x16_t{};
+                acc[2 * th + 1][u] = f32x16_t{};
+                const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
+                const bool full = n + 8 <= p.N;
+                // fast path: byte offset of row 8 i + L/8 of this slab, or out of range
+                const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 8 * i + rl;
+                    uint4 v = *reinterpret_cast<const uint4*>(stg + r * kStgRow + (cc << 4));
+                    if (FAST) {
+                        const uint32_t off = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), orr, off, 0, 0);
+                        continue;
+                    }
+                    const int ml = wm * 128 + 32 * u + r;
+                    const int64_t m = m0 + ml;
+                    if (m >= p.M || n >= p.N) continue;
+                    if (EPI == VDN_FP8_EPI_GATE) {
+                        const int64_t gi = p.gate_index ? min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1) : 0;
+                        const uint16_t* gp = p.gate + gi * p.ldgate + n;
+                        uint4 g;
+                        if (gate16 && full) g = *reinterpret_cast<const uint4*>(gp);
+                        else {
+                            const uint2 g0 = *reinterpret_cast<const uint2*>(gp);
+                            const uint2 g1 = full ? *reinterpret_cast<const uint2*>(gp + 4) : make_uint2(0u, 0u);
+                            g = make_uint4(g0.x, g0.y, g1.x, g1.y);
+                        }
+                        uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+                        if (p.residual) {
+                            const uint16_t* rp = p.residual + m * p.ldres + n;
+                            if (res16 && full) rv = *reinterpret_cast<const uint4*>(rp);
+                            else {
+                                const uint2 r0 = *reinterpret_cast<const uint2*>(rp);
+                                const uint2 r1 = full ? *reinterpret_cast<const uint2*>(rp + 4) : make_uint2(0u, 0u);
+                                rv = make_uint4(r0.x, r0.y, r1.x, r1.y);
+                            }
+                        }
+                        const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w},
+                                       rw[4] = {rv.x, rv.y, rv.z, rv.w};
+                        uint32_t o[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float lo = bf16_lo(vw[e]) * bf16_lo(gw[e]), hi = bf16_hi(vw[e]) * bf16_hi(gw[e]);
+                            if (p.residual) { lo += bf16_lo(rw[e]); hi += bf16_hi(rw[e]); }
+                            o[e] = pack_bf16x2(lo, hi);
+                        }
+                        v = make_uint4(o[0], o[1], o[2], o[3]);
+                    }
+                    uint16_t* dst = p.out + m * p.ldo + n;
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+                    if (full) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+                }
+                // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    // Prologue: the first tile's vectors, then blocks 0 and 1 of the stream.
+    producer_tile();
+    scal_copy(blockIdx.x, 0);
+#pragma unroll
+    for (int c = 0; c < kBlockCopies; ++c) copy(0, c);
+    advance();
+#pragma unroll
+    for (int c = 0; c < kBlockCopies; ++c) copy(1, c);
+    advance();
+
     i32x8_t w0[4], x0[4], w1[4], x1[4];
 #pragma unroll
-    for (int f = 0; f < 8; ++f) read_into(0, 0, f, w0, x0);
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][u] = f32x16_t{};   // the epilogue re-zeroes them per tile
+    int g = 0;    // stream index of the block being computed
+    int k = 0;    // tiles done by this workgroup
+    for (int tile = blockIdx.x; tile < T; tile += stride, ++k) {
+        int tm, tn;
+        tile_coords(tile, p.tiles_m, p.tiles_n, tm, tn);
+        const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+        // Block g has landed once only block g+1's copies -- and, after the first
+        // tile, the previous epilogue's stores -- may be pending.
+        if (k == 0) wave_sync<kBlockCopies>();
+        else wave_sync<kBlockCopies + kE>();
+        scal_copy(tile + stride, (k + 1) & 1);   // every wave is past the epilogue that used that buffer
+#pragma unroll
+        for (int f = 0; f < 8; ++f) read_into(g & 1, 0, f, w0, x0);
 
-    // One trip per block j, two half-steps of 16 MFMAs. With one wavefront per
-    // SIMD every stalled issue idles the matrix core, so each MFMA is followed
-    // by at most one copy and two fragment reads, in a fixed order:
-    //   half 0 (set 0): MFMAs 0-3 each read 2 fragments of block j half 1 into
-    //     set 1; after MFMA 7, barrier A (this wave's reads done, then all
-    //     waves): stage j % 2 is free; MFMAs 8-15 each issue one X copy of
-    //     block j+2 into it.
-    //   barrier B: this wave's copies of block j+1 have landed (only the 8
-    //     copies just issued may be pending), then all waves.
-    //   half 1 (set 1): MFMAs 0-7 each issue one W copy of block j+2; MFMAs 0-3
-    //     also read 2 fragments of block j+1 half 0 into set 0.
-    // A block's copies thus have 1.5 to 2 half-step pairs to land.
-    for (int j = 0; j < nk; ++j) {
+        for (int j = 0; j < nk; ++j, ++g) {
+            const int st = g & 1;
+            const bool more = j + 1 < nk;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            mfma(w0, x0, q);
-            fence();
-            if (q < 4) {
-                read_into(j, 1, 2 * q, w1, x1);
-                read_into(j, 1, 2 * q + 1, w1, x1);
+            for (int q = 0; q < 16; ++q) {
+                mfma(w0, x0, q);
+                fence();
+                if (q < 4) {
+                    read_into(st, 1, 2 * q, w1, x1);
+                    read_into(st, 1, 2 * q + 1, w1, x1);
+                }
+                if (q == 7) wave_sync<kNoVmWait>();
+                if (q >= 8) copy(st, q - 8);
+                fence();
             }
-            if (q == 7) wave_sync<kNoVmWait>();
-            if (q >= 8) copy(j + 2, q - 8);
-            fence();
-        }
-        wave_sync<kCopies>();
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            mfma(w1, x1, q);
-            fence();
-            if (q < 8) copy(j + 2, 8 + q);
-            if (q < 4) {
-                read_into(j + 1, 0, 2 * q, w0, x0);
-                read_into(j + 1, 0, 2 * q + 1, w0, x0);
+            for (int q = 0; q < 16; ++q) {
+                mfma(w1, x1, q);
+                fence();
+                if (q < 8) copy(st, 8 + q);
+                if (q == 7) {
+                    advance();
+                    // Block g+1 has landed: newer are block g+2's copies and, in a
+                    // tile's first block, the previous epilogue's stores and the
+                    // vector copy.
+                    if (j == 0 && k > 0) wave_sync<kBlockCopies + 1 + kE>();
+                    else if (j == 0) wave_sync<kBlockCopies + 1>();
+                    else wave_sync<kBlockCopies>();
+                }
+                if (q >= 8 && more) {
+                    read_into(st ^ 1, 0, 2 * (q - 8), w0, x0);
+                    read_into(st ^ 1, 0, 2 * (q - 8) + 1, w0, x0);
+                }
+                fence();
             }
-            fence();
         }
+        epilogue(m0, n0, k & 1);
     }
     // No copy may still be writing LDS when the workgroup ends.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
-
-    // Epilogue. acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4,
-    // m = wm*128 + 32 u + lane%32 (tile-relative). The results are finished in
-    // that layout (4 consecutive n per lane), staged through LDS -- free now --
-    // and written back as 16-byte pieces of whole 256-byte row segments: lane L
-    // of a store covers row 4 i + L/16, channels 8 (L%16) .. +7.
-    // Each wave stages its 128 x 128 quadrant (32 KiB) in its own LDS region,
-    // rows of 256 bytes; the 16-byte chunk c of row m sits at c ^ (m & 15) and its
-    // two 8-byte halves are swapped when (m >> 4) & 1 -- every 32-lane write
-    // then hits 32 distinct 8-byte bank pairs.
-    __builtin_amdgcn_s_barrier();          // every wave is done with the stages
-    asm volatile("" ::: "memory");
-    uint8_t* const tile_lds = smem + wave * 32768;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int ml = 32 * u + frow;
-        const int64_t m = min(m0 + wm * 128 + ml, p.M - 1);   // rows past M: computed, never stored
-        const float sxm = p.sx[m];
-        const uint16_t* grow = gate_row<EPI>(p, m);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int nl = 32 * t + 8 * q + 4 * fh;
-                const int64_t n = min(n0 + wn * 128 + nl, p.N - 4);
-                const float a4[4] = {acc[t][u][4 * q], acc[t][u][4 * q + 1], acc[t][u][4 * q + 2], acc[t][u][4 * q + 3]};
-                const uint2 v = epi4<EPI>(p, m, n, a4, sxm, grow);
-                const int c = nl >> 3, half = ((nl >> 2) & 1) ^ ((ml >> 4) & 1);
-                *reinterpret_cast<uint2*>(tile_lds + ml * 256 + ((c ^ (ml & 15)) << 4) + (half << 3)) = v;
-            }
-    }
-    const int64_t mq = m0 + wm * 128, nq = n0 + wn * 128;
-    const int rc = lane & 15;                          // 16-byte chunk of the row this lane stores
-    const int64_t n = nq + 8 * rc;
-    const bool vec16 = ((p.ldo & 7) == 0) && (((uintptr_t)p.out & 15) == 0);
-#pragma unroll 4
-    for (int i = 0; i < 32; ++i) {
-        const int ml = 4 * i + (lane >> 4);
-        uint4 v = *reinterpret_cast<const uint4*>(tile_lds + ml * 256 + ((rc ^ (ml & 15)) << 4));
-        if ((ml >> 4) & 1) v = make_uint4(v.z, v.w, v.x, v.y);
-        const int64_t m = mq + ml;
-        if (m >= p.M || n >= p.N) continue;
-        uint16_t* dst = p.out + m * p.ldo + n;
-        if (vec16 && n + 8 <= p.N) {
-            *reinterpret_cast<uint4*>(dst) = v;
-        } else {
-            *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
-            if (n + 8 <= p.N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -475,6 +642,20 @@ void k_gemm_fp8_ktail(GemmArgs p)
 
 bool aligned(const void* q, uintptr_t a) { return ((uintptr_t)q % a) == 0; }
 
+// Compute units of the current device (the persistent kernel's grid), cached per
+// device; 0 if the runtime cannot say.
+int device_cus()
+{
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cached[dev] = n;
+    return n;
+}
+
 }  // namespace
 }  // namespace vdn
 
@@ -494,8 +675,9 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
         return set_error(VDN_FP8_EINVAL, "gemm: need ldx, ldw >= K and multiples of 16, ldo >= N and a multiple of 4");
     if (ldx * 256 > (int64_t)0x7fffffff || ldw * 256 > (int64_t)0x7fffffff)
         return set_error(VDN_FP8_EINVAL, "gemm: row stride too large (256 rows must span < 2 GiB)");
-    if (!aligned(xq, 16) || !aligned(wq, 16) || !aligned(out, 8) || !aligned(w_scale, 16) || (bias && !aligned(bias, 8)))
-        return set_error(VDN_FP8_EINVAL, "gemm: misaligned operand (xq, wq 16 B; w_scale 16 B; out, bias 8 B)");
+    if (!aligned(xq, 16) || !aligned(wq, 16) || !aligned(out, 8) || !aligned(w_scale, 16) || !aligned(x_scale, 16) ||
+        (bias && !aligned(bias, 16)) || (gate_index && !aligned(gate_index, 16)))
+        return set_error(VDN_FP8_EINVAL, "gemm: misaligned operand (xq, wq, x_scale, w_scale, bias, gate_index 16 B; out 8 B)");
     if (epilogue == VDN_FP8_EPI_GATE) {
         if (!gate || gate_rows < 1) return set_error(VDN_FP8_EINVAL, "gemm: the gate epilogue needs a gate table of >= 1 row");
         if (ldgate < N || ldgate % 4 || !aligned(gate, 8)) return set_error(VDN_FP8_EINVAL, "gemm: gate rows must be >= N and 8-byte aligned");
@@ -509,12 +691,22 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     GemmArgs p{(const uint8_t*)xq, x_scale, (const uint8_t*)wq, w_scale, M, N, K, ldx, ldw,
                (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
                (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n};
-    const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
     const bool main = (K % mainloop::BK) == 0;
-#define VDN_LAUNCH(E)                                                                   \
-    do {                                                                                \
-        if (main) hipLaunchKernelGGL((k_gemm_fp8<E>), grid, block, 0, stream, p);       \
-        else hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);      \
+    int64_t blocks = tiles_m * tiles_n;
+    if (main) {
+        const int cus = device_cus();
+        if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "gemm: cannot query the device's compute units");
+        blocks = std::min<int64_t>(blocks, cus);
+    }
+    const dim3 grid((unsigned)blocks), block(kThreads);
+    // the fast epilogue: 16-byte output rows, no gate, row offsets within 31 bits
+    const bool fast = epilogue != VDN_FP8_EPI_GATE && N % 8 == 0 && ldo % 8 == 0 && aligned(out, 16) &&
+                      (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
+#define VDN_LAUNCH(E)                                                                          \
+    do {                                                                                       \
+        if (main && fast) hipLaunchKernelGGL((k_gemm_fp8<E, true>), grid, block, 0, stream, p);  \
+        else if (main) hipLaunchKernelGGL((k_gemm_fp8<E, false>), grid, block, 0, stream, p);    \
+        else hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);             \
     } while (0)
     switch (epilogue) {
         case VDN_FP8_EPI_NONE: VDN_LAUNCH(VDN_FP8_EPI_NONE); break;

@@ -49,6 +49,12 @@ def _ptr(t):
     return t.data_ptr() if t is not None else None
 
 
+def _aligned16(t):
+    """t itself when its data starts on a 16-byte boundary (the GEMM reads its
+    vectors 16 bytes at a time), else a fresh copy, which the allocator aligns."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _rows(x):
     """The reference's input check (fp8_linear.py:102-107): GPU, 2-D, then contiguous."""
     if not x.is_cuda:
@@ -220,7 +226,8 @@ class Fp8Linear(nn.Module):
                              "the sm100 branch, not built for gfx950)")
         if x_fp8.stride(1) != 1:
             x_fp8 = x_fp8.contiguous()
-        x_scale = x_scale.contiguous()
+        x_fp8 = _aligned16(x_fp8)
+        x_scale = _aligned16(x_scale.contiguous())
         dev = x_fp8.device
         out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
         epi = _EPILOGUES.get(epilogue)
@@ -230,7 +237,7 @@ class Fp8Linear(nn.Module):
         if bias is not None:
             if bias.dtype != torch.bfloat16 or bias.numel() != N:
                 raise ValueError("the fused bias must be a bfloat16 [N] tensor")
-            bias = bias.detach().contiguous()
+            bias = _aligned16(bias.detach().contiguous())
         g = gi = res = None
         ldgate = ldres = grows = 0
         if epi == _lib.EPI_GATE:
@@ -241,7 +248,7 @@ class Fp8Linear(nn.Module):
                 g = g.to(torch.bfloat16).contiguous()
             ldgate, grows = g.stride(0), g.shape[0]
             if gate_index is not None:
-                gi = gate_index.to(device=dev, dtype=torch.int32).contiguous()
+                gi = _aligned16(gate_index.to(device=dev, dtype=torch.int32).contiguous())
                 if gi.numel() != M:
                     raise ValueError("gate_index must hold one table row per token")
             if residual is not None:
