@@ -72,6 +72,9 @@ struct GemmArgs {
     uint16_t* out;
     int64_t ldo;
     int tiles_m, tiles_n;
+    // K-block rotation: tile (tm, tn) walks its K blocks starting at block
+    // ((tm + tn) % k_phase_mod) * k_phase_step (mod nk); 0 = no rotation.
+    int k_phase_mod, k_phase_step;
 };
 
 // gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3)
@@ -277,15 +280,17 @@ void k_gemm_fp8(GemmArgs p)
     // Producer: the next block to copy is block pj of tile ptile. Blocks of
     // tiles past the end still issue their copies, through empty descriptors
     // (zeros, no memory read), so the vmcnt bookkeeping stays fixed.
-    int ptile = blockIdx.x, pj = 0;
+    int ptile = blockIdx.x, pj = 0, pphase = 0, pkb = 0;
     i32x4_t xr, wr;
     auto producer_tile = [&]() {
         int64_t xb = 0, wb = 0;
         const uint8_t* xa = p.xq;
         const uint8_t* wa = p.wq;
+        pphase = 0;
         if (ptile < T) {
             int tm, tn;
             tile_coords(ptile, p.tiles_m, p.tiles_n, tm, tn);
+            if (p.k_phase_mod > 0) pphase = (((tm + tn) % p.k_phase_mod) * p.k_phase_step) % nk;
             const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
             xa += m0 * p.ldx;
             wa += n0 * p.ldw;
@@ -294,13 +299,14 @@ void k_gemm_fp8(GemmArgs p)
         }
         xr = rsrc_words(xa, xb);
         wr = rsrc_words(wa, wb);
+        pkb = pphase * BK;
         asm volatile("s_nop 4");   // SGPR write by VALU -> use as a buffer descriptor
     };
     // Copy c (0..15) of the producer's block into stage st: c < 8 is X rows
     // 64 wave + 8 c .., else W rows.
     auto copy = [&](int st, int c) {
         const uint32_t dst = lds_base + (uint32_t)st * kStage;
-        const uint32_t kb = (uint32_t)pj * BK;
+        const uint32_t kb = (uint32_t)pkb;
         const int i = c & 7;
         if (c < 8) copy16_to_lds(xr, dst + (64 * wave + 8 * i) * BK, xoff[i], kb);
         else copy16_to_lds(wr, dst + BM * BK + (64 * wave + 8 * i) * BK, woff[i], kb);
@@ -310,6 +316,9 @@ void k_gemm_fp8(GemmArgs p)
             pj = 0;
             ptile += stride;
             producer_tile();
+        } else {
+            const int kbi = pj + pphase;
+            pkb = (kbi >= nk ? kbi - nk : kbi) * BK;
         }
     };
     // The vectors of the k-th tile of this workgroup go to scalar buffer k % 2:
@@ -642,6 +651,12 @@ void k_gemm_fp8_ktail(GemmArgs p)
 
 bool aligned(const void* q, uintptr_t a) { return ((uintptr_t)q % a) == 0; }
 
+// K-block rotation of the main kernel: tiles with (tm + tn) odd start one block
+// later, so the workgroups sharing an X or W panel do not all miss the same
+// lines at once (and strided rows do not hit the same memory channels in
+// lockstep). Measured on the QKV and FFN-down shapes; (4, 2) is as good.
+constexpr int kPhaseMod = 2, kPhaseStep = 1;
+
 // Compute units of the current device (the persistent kernel's grid), cached per
 // device; 0 if the runtime cannot say.
 int device_cus()
@@ -690,7 +705,8 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     if (tiles_m * tiles_n > (int64_t)INT32_MAX / 2) return set_error(VDN_FP8_EINVAL, "gemm: problem too large");
     GemmArgs p{(const uint8_t*)xq, x_scale, (const uint8_t*)wq, w_scale, M, N, K, ldx, ldw,
                (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
-               (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n};
+               (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n,
+               kPhaseMod, kPhaseStep};
     const bool main = (K % mainloop::BK) == 0;
     int64_t blocks = tiles_m * tiles_n;
     if (main) {
