@@ -48,26 +48,54 @@ struct Args {
     uint16_t* w_merged;  // nullable, row stride ldw
 };
 
-// Stages A[:, k0 : k0 + kChunk] (rows j < RP, zero beyond rank and K) in LDS.
+// A[:, k0 : k0 + kChunk] (rows j < RP, zero beyond rank and K) travels to LDS in
+// two halves, so the global loads of the next step can be in flight while the
+// current step computes: load_a fills this thread's pieces, store_a writes them.
+template <int RP>
+struct APieces {
+    static constexpr int kPieces = RP * (kChunk / 4);               // 8-byte pieces
+    static constexpr int kPerThread = kPieces / (kWaves * kLanes);  // RP / 16
+    uint2 v[kPerThread];
+};
+
+template <int RP>
+__device__ __forceinline__ void load_a(const Args& p, APieces<RP>& a, int64_t k0)
+{
+#pragma unroll
+    for (int i = 0; i < APieces<RP>::kPerThread; ++i) {
+        const int q = (int)threadIdx.x + i * kWaves * kLanes;
+        const int j = q / (kChunk / 4), c4 = (q % (kChunk / 4)) * 4;
+        const int64_t k = k0 + c4;
+        a.v[i] = make_uint2(0u, 0u);
+        if (j < p.rank && k < p.K) a.v[i] = *reinterpret_cast<const uint2*>(p.a + (int64_t)j * p.K + k);
+    }
+}
+
+template <int RP>
+__device__ __forceinline__ void store_a(const APieces<RP>& a, uint16_t* sA)
+{
+#pragma unroll
+    for (int i = 0; i < APieces<RP>::kPerThread; ++i) {
+        const int q = (int)threadIdx.x + i * kWaves * kLanes;
+        const int j = q / (kChunk / 4), c4 = (q % (kChunk / 4)) * 4;
+        *reinterpret_cast<uint2*>(sA + j * kStride + c4) = a.v[i];
+    }
+}
+
 template <int RP>
 __device__ __forceinline__ void stage_a(const Args& p, uint16_t* sA, int64_t k0)
 {
-    constexpr int kPieces = RP * (kChunk / 4);  // 8-byte pieces
-    for (int q = threadIdx.x; q < kPieces; q += kWaves * kLanes) {
-        const int j = q / (kChunk / 4), c4 = (q % (kChunk / 4)) * 4;
-        const int64_t k = k0 + c4;
-        uint2 v = make_uint2(0u, 0u);
-        if (j < p.rank && k < p.K) v = *reinterpret_cast<const uint2*>(p.a + (int64_t)j * p.K + k);
-        *reinterpret_cast<uint2*>(sA + j * kStride + c4) = v;
-    }
+    APieces<RP> a;
+    load_a<RP>(p, a, k0);
+    store_a<RP>(a, sA);
 }
 
 // One 16x16 tile of W' for this wave: columns kt .. kt+15 of rows n0 .. n0+15.
 // Returns the lane's 4 values (k = kt + 4*(lane/16) + i, n = n0 + lane%16)
 // packed as bf16 pairs.
 template <int RP>
-__device__ __forceinline__ uint2 merged_tile(const Args& p, const uint16_t* sA, int col, int64_t kt,
-                                             int64_t n, bool nvalid, const bf16x8_t* bop)
+__device__ __forceinline__ uint2 merged_tile(const Args& p, const uint16_t* sA, int col, uint2 w4,
+                                             const bf16x8_t* bop)
 {
     const int lane = threadIdx.x & (kLanes - 1);
     const int nl = lane & 15, g = lane >> 4;
@@ -85,8 +113,6 @@ __device__ __forceinline__ uint2 merged_tile(const Args& p, const uint16_t* sA, 
         const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[s], acc, 0, 0, 0);
     }
-    uint2 w4 = make_uint2(0u, 0u);
-    if (nvalid) w4 = *reinterpret_cast<const uint2*>(p.w + n * p.ldw + kt + 4 * g);
     // delta.to(bf16), then the bf16 add: binary32 add of the two bf16 values, rounded.
     const float d0 = round_bf16(acc[0] * p.lora_scale), d1 = round_bf16(acc[1] * p.lora_scale);
     const float d2 = round_bf16(acc[2] * p.lora_scale), d3 = round_bf16(acc[3] * p.lora_scale);
@@ -113,7 +139,7 @@ __device__ __forceinline__ uint32_t codes4_exact(uint2 v, float s)
 template <int RP, int NRES>
 __global__ __launch_bounds__(kWaves * kLanes) void k_lora_requant(Args p)
 {
-    __shared__ uint16_t sA[RP * kStride];
+    __shared__ uint16_t sA[2][RP * kStride];
     __shared__ uint32_t sMax[kWaves][kRows];
 
     const int wave = threadIdx.x / kLanes, lane = threadIdx.x & (kLanes - 1);
@@ -138,17 +164,41 @@ __global__ __launch_bounds__(kWaves * kLanes) void k_lora_requant(Args p)
         bop[s] = __builtin_bit_cast(bf16x8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
     }
 
-    // Merge only (no codes wanted): one sweep that writes W'.
+    // This lane's W values (rows n, columns step*kChunk + wave*16 + 4g .. +3) for
+    // every step are loaded up front when they fit in registers, so no step
+    // waits on HBM; A goes through two LDS buffers, the next step's global
+    // loads in flight while the current step computes.
     const bool merge_only = p.wq == nullptr;
+    auto w_at = [&](int64_t step) {
+        const int64_t kt = step * kChunk + wave * 16;
+        uint2 w4 = make_uint2(0u, 0u);
+        if (nvalid && kt < p.K) w4 = *reinterpret_cast<const uint2*>(p.w + n * p.ldw + kt + 4 * g);
+        return w4;
+    };
     uint2 res[NRES > 0 ? NRES : 1];
+    if constexpr (NRES > 0) {
+#pragma unroll
+        for (int i = 0; i < NRES; ++i)
+            if (i < steps) res[i] = w_at(i);
+    }
     uint32_t m2 = 0;
+    stage_a<RP>(p, sA[0], 0);
+    __syncthreads();
     for (int64_t step = 0; step < steps; ++step) {
-        const int64_t k0 = step * kChunk;
-        stage_a<RP>(p, sA, k0);
-        __syncthreads();
-        const int64_t kt = k0 + wave * 16;
+        APieces<RP> next;
+        const bool more = step + 1 < steps;
+        if (more) load_a<RP>(p, next, (step + 1) * kChunk);
+        const int64_t kt = step * kChunk + wave * 16;
+        uint2 w4 = make_uint2(0u, 0u);
+        if constexpr (NRES > 0) {
+#pragma unroll
+            for (int i = 0; i < NRES; ++i)
+                if (i == step) w4 = res[i];
+        } else {
+            w4 = w_at(step);
+        }
         uint2 t = make_uint2(0u, 0u);
-        if (kt < p.K) t = merged_tile<RP>(p, sA, wave * 16, kt, n, nvalid, bop);
+        if (kt < p.K) t = merged_tile<RP>(p, sA[step & 1], wave * 16, w4, bop);
         if (merge_only) {
             if (kt < p.K && nvalid) *reinterpret_cast<uint2*>(p.w_merged + n * p.ldw + kt + 4 * g) = t;
         } else {
@@ -160,6 +210,7 @@ __global__ __launch_bounds__(kWaves * kLanes) void k_lora_requant(Args p)
                     if (i == step) res[i] = t;
             }
         }
+        if (more) store_a<RP>(next, sA[(step + 1) & 1]);
         __syncthreads();
     }
     if (merge_only) return;
@@ -187,9 +238,9 @@ __global__ __launch_bounds__(kWaves * kLanes) void k_lora_requant(Args p)
             for (int i = 0; i < NRES; ++i)
                 if (i == step) t = res[i];
         } else {
-            stage_a<RP>(p, sA, step * kChunk);
+            stage_a<RP>(p, sA[0], step * kChunk);
             __syncthreads();
-            if (kt < p.K) t = merged_tile<RP>(p, sA, wave * 16, kt, n, nvalid, bop);
+            if (kt < p.K) t = merged_tile<RP>(p, sA[0], wave * 16, w_at(step), bop);
             __syncthreads();
         }
         if (kt < p.K && nvalid) {
@@ -204,10 +255,13 @@ void launch_rp(const Args& p, dim3 grid, hipStream_t st)
 {
     const dim3 block(kWaves * kLanes);
     const int64_t steps = (p.K + kChunk - 1) / kChunk;
+    // W' stays in registers for up to kMaxRes steps (what fits in the 128 VGPRs
+    // of a 1024-thread workgroup next to the rank-RP operand); wider rows recompute.
+    constexpr int kMaxRes = RP >= 96 ? 12 : 20;
     if (steps <= 8) hipLaunchKernelGGL((k_lora_requant<RP, 8>), grid, block, 0, st, p);
-    else if (steps <= 16) hipLaunchKernelGGL((k_lora_requant<RP, 16>), grid, block, 0, st, p);
-    else if (steps <= 24) hipLaunchKernelGGL((k_lora_requant<RP, 24>), grid, block, 0, st, p);
-    else if (steps <= 32) hipLaunchKernelGGL((k_lora_requant<RP, 32>), grid, block, 0, st, p);
+    else if (steps <= 12) hipLaunchKernelGGL((k_lora_requant<RP, 12>), grid, block, 0, st, p);
+    else if (steps <= 16 && kMaxRes >= 16) hipLaunchKernelGGL((k_lora_requant<RP, (kMaxRes >= 16 ? 16 : 0)>), grid, block, 0, st, p);
+    else if (steps <= 20 && kMaxRes >= 20) hipLaunchKernelGGL((k_lora_requant<RP, (kMaxRes >= 20 ? 20 : 0)>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((k_lora_requant<RP, 0>), grid, block, 0, st, p);
 }
 
