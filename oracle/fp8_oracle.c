@@ -13,7 +13,7 @@
  * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off, never -ffast-math:
  * contraction or reassociation would change the binary32 results).
  *
- * How each function is pinned (checked by tests/test_oracle_*.py):
+ * How each function is pinned (checked by tests/test_oracle.py):
  *   oracle_e4m3_from_f32   exhaustive over all bf16 patterns and over every
  *                          e4m3 rounding midpoint +-1 ulp against torch's CPU
  *                          cast and against a nearest-value brute force over
