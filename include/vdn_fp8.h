@@ -81,7 +81,9 @@ int vdn_fp8_swiglu_quantize_rows(const void *h, int64_t M, int64_t K, int64_t ld
  *           src/models/ops/fp8_linear.py:262-267, preceded by the update of
  *           merge_lora_state, src/inference/utils/lora.py:80-94.
  * Requires: K % 8 == 0, ldw % 8 == 0, ldq % 8 == 0; with LoRA: 1 <= rank <= 128,
- *           K % 16 == 0, lora_a 8-byte aligned, wq rows 4-byte aligned.
+ *           K % 16 == 0, lora_a 16-byte aligned, wq rows 4-byte aligned. With
+ *           LoRA and codes, w_scale holds the row maxima between the kernels of
+ *           the call (it is the only scratch the call needs).
  */
 int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
                               const void *lora_a, const void *lora_b, int64_t rank,
