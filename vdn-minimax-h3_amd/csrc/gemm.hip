@@ -49,7 +49,7 @@ namespace {
 constexpr int BM = 256;        // tokens per tile
 constexpr int BN = 256;        // output channels per tile
 constexpr int kThreads = 256;  // 4 wavefronts, 2 (n) x 2 (m), 128 x 128 each
-constexpr int kGroupM = 8;
+constexpr int kGroupM = 4;     // m-tiles per group of the tile order (GemmArgs::group_m)
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
@@ -75,6 +75,7 @@ struct GemmArgs {
     // K-block rotation: tile (tm, tn) walks its K blocks starting at block
     // ((tm + tn) % k_phase_mod) * k_phase_step (mod nk); 0 = no rotation.
     int k_phase_mod, k_phase_step;
+    int group_m;   // m-tiles per group of the tile order
 };
 
 // gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3)
@@ -85,15 +86,15 @@ __device__ __forceinline__ float gelu_tanh(float v)
 }
 
 // Renumbers workgroup b so that XCD (b % 8) gets a contiguous run of tiles,
-// then maps the run index to (tile_m, tile_n) in groups of kGroupM m-tiles.
-__device__ __forceinline__ void tile_coords(int b, int tiles_m, int tiles_n, int& tm, int& tn)
+// then maps the run index to (tile_m, tile_n) in groups of gm m-tiles.
+__device__ __forceinline__ void tile_coords(int b, int tiles_m, int tiles_n, int gm, int& tm, int& tn)
 {
     const int T = tiles_m * tiles_n;
     const int q = T / 8, r = T % 8, xcd = b % 8, local = b / 8;
     const int t = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
-    const int group = kGroupM * tiles_n;
-    const int first_m = (t / group) * kGroupM;
-    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int group = gm * tiles_n;
+    const int first_m = (t / group) * gm;
+    const int gsize = min(tiles_m - first_m, gm);
     tm = first_m + (t % group) % gsize;
     tn = (t % group) / gsize;
 }
@@ -201,6 +202,17 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// As wave_sync, without waiting for this wave's LDS reads.
+template <int VM>
+__device__ __forceinline__ void wave_sync_vm()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------------------
 // main kernel: K % 128 == 0, persistent
 // ---------------------------------------------------------------------------
@@ -216,6 +228,8 @@ constexpr int kStgWave = 32 * kStgRow;      // 32 rows per wave
 constexpr int kStg = kScal + 8192;          // epilogue staging
 constexpr int kLds = kStg + 4 * kStgWave;   // 154 KiB
 constexpr int kEpiStores = 32;              // 16-byte stores per wave per tile (fast epilogue)
+constexpr int kStoreNT = 2;                 // cache policy of the output stores: non-temporal (the
+                                            // output streams; keeps L2 for the operand panels)
 
 // Row r, 16-byte chunk c (0..7) of a tile sits at chunk c ^ ((r >> 1) & 7) of
 // its 128-byte LDS row.
@@ -236,10 +250,12 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // two blocks are in flight while this tile's epilogue runs. Per block g (stage
 // g % 2), two half-steps of 16 MFMAs:
 //   half 0: MFMAs 0-3 read the half-1 fragments of g; barrier A after MFMA 7
-//     (stage g % 2 is then free); MFMAs 8-15 issue the X copies of block g+2.
-//   half 1: MFMAs 0-7 issue the W copies of block g+2; barrier B after MFMA 7:
-//     this wave's copies of block g+1 have landed (newer ones may be pending),
-//     then all waves; MFMAs 8-15 read the half-0 fragments of g+1.
+//     (stage g % 2 is then free); MFMAs 8-15 issue the W copies of block g+2.
+//   half 1: MFMAs 0-7 issue the X copies of block g+2; after MFMA 7 this
+//     wave's W copies of block g+1 have landed (newer ones may be pending) and
+//     all waves meet (barrier B); MFMAs 8-11 read the W fragments of g+1's
+//     first half; after MFMA 11 the same for its X copies (barrier C); MFMAs
+//     12-15 read its X fragments. W goes first because it is read first.
 // A tile's vectors (w_scale, x_scale, bias, gate rows) are copied into one of
 // two scalar buffers at the start of the tile before, one copy per wave. The
 // epilogue stages through LDS of its own.
@@ -289,7 +305,7 @@ void k_gemm_fp8(GemmArgs p)
         pphase = 0;
         if (ptile < T) {
             int tm, tn;
-            tile_coords(ptile, p.tiles_m, p.tiles_n, tm, tn);
+            tile_coords(ptile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
             if (p.k_phase_mod > 0) pphase = (((tm + tn) % p.k_phase_mod) * p.k_phase_step) % nk;
             const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
             xa += m0 * p.ldx;
@@ -329,7 +345,7 @@ void k_gemm_fp8(GemmArgs p)
         int64_t bytes = 0;
         if (t < T) {
             int tm, tn;
-            tile_coords(t, p.tiles_m, p.tiles_n, tm, tn);
+            tile_coords(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
             const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
             if (wave == 0) { base = p.sw + n0; bytes = min(p.N - n0, (int64_t)256) * 4; }
             else if (wave == 1) { base = p.sx + m0; bytes = min(p.M - m0, (int64_t)256) * 4; }
@@ -439,7 +455,7 @@ void k_gemm_fp8(GemmArgs p)
                     uint4 v = *reinterpret_cast<const uint4*>(stg + r * kStgRow + (cc << 4));
                     if (FAST) {
                         const uint32_t off = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), orr, off, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), orr, off, 0, kStoreNT);
                         continue;
                     }
                     const int ml = wm * 128 + 32 * u + r;
@@ -489,11 +505,12 @@ void k_gemm_fp8(GemmArgs p)
     // Prologue: the first tile's vectors, then blocks 0 and 1 of the stream.
     producer_tile();
     scal_copy(blockIdx.x, 0);
+    // W copies (c = 8..15) before X copies (c = 0..7), as in the loop
 #pragma unroll
-    for (int c = 0; c < kBlockCopies; ++c) copy(0, c);
+    for (int c = 0; c < kBlockCopies; ++c) copy(0, (c + kCopies) % kBlockCopies);
     advance();
 #pragma unroll
-    for (int c = 0; c < kBlockCopies; ++c) copy(1, c);
+    for (int c = 0; c < kBlockCopies; ++c) copy(1, (c + kCopies) % kBlockCopies);
     advance();
 
     i32x8_t w0[4], x0[4], w1[4], x1[4];
@@ -505,7 +522,7 @@ void k_gemm_fp8(GemmArgs p)
     int k = 0;    // tiles done by this workgroup
     for (int tile = blockIdx.x; tile < T; tile += stride, ++k) {
         int tm, tn;
-        tile_coords(tile, p.tiles_m, p.tiles_n, tm, tn);
+        tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
         // Block g has landed once only block g+1's copies -- and, after the first
         // tile, the previous epilogue's stores -- may be pending.
@@ -527,27 +544,30 @@ void k_gemm_fp8(GemmArgs p)
                     read_into(st, 1, 2 * q + 1, w1, x1);
                 }
                 if (q == 7) wave_sync<kNoVmWait>();
-                if (q >= 8) copy(st, q - 8);
+                if (q >= 8) copy(st, q);             // W copies of block g+2
                 fence();
             }
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 mfma(w1, x1, q);
                 fence();
-                if (q < 8) copy(st, 8 + q);
+                if (q < 8) copy(st, q);              // X copies of block g+2
                 if (q == 7) {
                     advance();
-                    // Block g+1 has landed: newer are block g+2's copies and, in a
-                    // tile's first block, the previous epilogue's stores and the
-                    // vector copy.
-                    if (j == 0 && k > 0) wave_sync<kBlockCopies + 1 + kE>();
-                    else if (j == 0) wave_sync<kBlockCopies + 1>();
-                    else wave_sync<kBlockCopies>();
+                    // W of block g+1 has landed: newer are its X copies, block g+2's
+                    // copies and, in a tile's first block, the previous epilogue's
+                    // stores and the vector copy.
+                    if (j == 0 && k > 0) wave_sync<kCopies + kBlockCopies + 1 + kE>();
+                    else if (j == 0) wave_sync<kCopies + kBlockCopies + 1>();
+                    else wave_sync<kCopies + kBlockCopies>();
                 }
-                if (q >= 8 && more) {
-                    read_into(st ^ 1, 0, 2 * (q - 8), w0, x0);
-                    read_into(st ^ 1, 0, 2 * (q - 8) + 1, w0, x0);
+                if (q == 11) {
+                    // X of block g+1 has landed
+                    if (j == 0 && k > 0) wave_sync_vm<kBlockCopies + 1 + kE>();
+                    else if (j == 0) wave_sync_vm<kBlockCopies + 1>();
+                    else wave_sync_vm<kBlockCopies>();
                 }
+                if (q >= 8 && more) read_into(st ^ 1, 0, q - 8, w0, x0);   // W fragments, then X
                 fence();
             }
         }
@@ -578,7 +598,7 @@ void k_gemm_fp8_ktail(GemmArgs p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
     int tm, tn;
-    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int nk = (int)((p.K + BK - 1) / BK);
 
@@ -706,7 +726,7 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     GemmArgs p{(const uint8_t*)xq, x_scale, (const uint8_t*)wq, w_scale, M, N, K, ldx, ldw,
                (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
                (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n,
-               kPhaseMod, kPhaseStep};
+               kPhaseMod, kPhaseStep, kGroupM};
     const bool main = (K % mainloop::BK) == 0;
     int64_t blocks = tiles_m * tiles_n;
     if (main) {
