@@ -260,7 +260,8 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // two scalar buffers at the start of the tile before, one copy per wave. The
 // epilogue stages through LDS of its own.
 //
-// FAST (no gate epilogue, 16-byte aligned output rows): the epilogue issues
+// FAST (16-byte aligned output rows; no per-row gate and no residual -- a
+// broadcast gate row travels with the tile's vectors): the epilogue issues
 // exactly kEpiStores buffer stores per wave, columns past N sent out of range
 // (dropped), so the waits that follow count them and the stores drain while
 // the next tile runs. Otherwise the waits also cover the epilogue's memory
@@ -339,7 +340,8 @@ void k_gemm_fp8(GemmArgs p)
     };
     // The vectors of the k-th tile of this workgroup go to scalar buffer k % 2:
     // wave 0 w_scale[n0 ..+255], wave 1 x_scale[m0 ..+255], wave 2 bias[n0 ..+511]
-    // (256 used), wave 3 gate_index[m0 ..+255]. Missing ones read as zeros.
+    // (256 used), wave 3 gate_index[m0 ..+255] -- or, for a broadcast gate on the
+    // fast path, the gate row gate[0][n0 ..+511]. Missing ones read as zeros.
     auto scal_copy = [&](int t, int buf) {
         const void* base = p.sx;
         int64_t bytes = 0;
@@ -350,6 +352,7 @@ void k_gemm_fp8(GemmArgs p)
             if (wave == 0) { base = p.sw + n0; bytes = min(p.N - n0, (int64_t)256) * 4; }
             else if (wave == 1) { base = p.sx + m0; bytes = min(p.M - m0, (int64_t)256) * 4; }
             else if (wave == 2) { if (p.bias) { base = p.bias + n0; bytes = min(p.N - n0, (int64_t)512) * 2; } }
+            else if (EPI == VDN_FP8_EPI_GATE && FAST) { base = p.gate + n0; bytes = min(p.N - n0, (int64_t)512) * 2; }
             else if (p.gate_index) { base = p.gate_index + m0; bytes = min(p.M - m0, (int64_t)256) * 4; }
         }
         const i32x4_t r = rsrc_words(base, bytes);
@@ -408,6 +411,7 @@ void k_gemm_fp8(GemmArgs p)
         const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
         const uint16_t* s_bias = reinterpret_cast<const uint16_t*>(scal + 2048);
         const int32_t* s_gi = reinterpret_cast<const int32_t*>(scal + 3072);
+        const uint16_t* s_gate = reinterpret_cast<const uint16_t*>(scal + 3072);
         uint8_t* const stg = smem + kStg + wave * kStgWave;
         const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(p.out + m0 * p.ldo), 0, (int)min(min(p.M - m0, (int64_t)BM) * p.ldo * 2, (int64_t)0x7fffffff), kRsrcWord3);
@@ -439,6 +443,10 @@ void k_gemm_fp8(GemmArgs p)
 #pragma unroll
                             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
                         }
+                        if (EPI == VDN_FP8_EPI_GATE && FAST) {   // broadcast gate row, no residual
+                            const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
+                            v[0] *= bf16_lo(gv.x); v[1] *= bf16_hi(gv.x); v[2] *= bf16_lo(gv.y); v[3] *= bf16_hi(gv.y);
+                        }
                         *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) =
                             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     }
@@ -461,7 +469,7 @@ void k_gemm_fp8(GemmArgs p)
                     const int ml = wm * 128 + 32 * u + r;
                     const int64_t m = m0 + ml;
                     if (m >= p.M || n >= p.N) continue;
-                    if (EPI == VDN_FP8_EPI_GATE) {
+                    if (EPI == VDN_FP8_EPI_GATE && !FAST) {
                         const int64_t gi = p.gate_index ? min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1) : 0;
                         const uint16_t* gp = p.gate + gi * p.ldgate + n;
                         uint4 g;
@@ -735,9 +743,12 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
         blocks = std::min<int64_t>(blocks, cus);
     }
     const dim3 grid((unsigned)blocks), block(kThreads);
-    // the fast epilogue: 16-byte output rows, no gate, row offsets within 31 bits
-    const bool fast = epilogue != VDN_FP8_EPI_GATE && N % 8 == 0 && ldo % 8 == 0 && aligned(out, 16) &&
-                      (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
+    // the fast epilogue: 16-byte output rows, row offsets within 31 bits, and no
+    // per-row gate or residual (a gate table of one row is staged like the bias)
+    const bool gate_broadcast = epilogue == VDN_FP8_EPI_GATE && !residual && (gate_rows == 1 || !gate_index) &&
+                                aligned(gate, 16);
+    const bool fast = (epilogue != VDN_FP8_EPI_GATE || gate_broadcast) && N % 8 == 0 && ldo % 8 == 0 &&
+                      aligned(out, 16) && (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
 #define VDN_LAUNCH(E)                                                                          \
     do {                                                                                       \
         if (main && fast) hipLaunchKernelGGL((k_gemm_fp8<E, true>), grid, block, 0, stream, p);  \
