@@ -46,8 +46,11 @@ def _gpu_clock():
 
 
 def _time_region(fn, reps):
-    """Mean ms of fn() over reps launches, from HIP events on the current stream."""
+    """Mean ms of fn() over reps launches, from HIP events on the current stream (after one
+    untimed call)."""
     import torch
+    fn()
+    torch.cuda.synchronize()
     ev = _events(2 * reps)
     for i in range(reps):
         ev[2 * i].record()
@@ -216,6 +219,15 @@ def main():
         ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
         extra["quantize_rows_13824"] = {"ms": round(ms, 4),
                                         "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
+        # the block's pre-norm (RMSNorm + AdaLN affine, table of 2 rows) fused with the quantizer
+        g = torch.Generator().manual_seed(6)
+        nw = (1 + 0.05 * torch.randn(K, generator=g)).to(torch.bfloat16).to(dev)
+        nsc = (0.2 * torch.randn(2, K, generator=g)).to(torch.bfloat16).to(dev)
+        nsh = (0.2 * torch.randn(2, K, generator=g)).to(torch.bfloat16).to(dev)
+        nidx = torch.randint(0, 2, (M,), generator=g).to(torch.int32).to(dev)
+        ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
+        extra["pre_norm_quantize"] = {"ms": round(ms, 4),
+                                      "GB/s": round(wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9, 1)}
         extra["gpu_clock"] = _gpu_clock()
     line["extra"] = extra
     if not args.no_cpu_baseline:

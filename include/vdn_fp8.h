@@ -67,6 +67,29 @@ int vdn_fp8_swiglu_quantize_rows(const void *h, int64_t M, int64_t K, int64_t ld
                                  void *y, int64_t ldy, float *scale, hipStream_t stream);
 
 /*
+ * Pre-norm of a DiT block fused with the per-token quantization of its output:
+ *   rstd   = 1 / sqrt(sum_k x[m][k]^2 / K + eps)                     (binary32)
+ *   n[m][k] = bf16(((x[m][k] * rstd) * weight[k]) * (1 + scale[i][k]) + shift[i][k])
+ *   y, y_scale = the quantize_rows arithmetic on n               (codes exact given n)
+ * with i = mod_index[m] clamped into [0, mod_rows) (row 0 when mod_index is
+ * NULL). The chain runs in binary32 with one rounding at the end, as the
+ * compiled `pre` of the reference does. weight may be NULL (no weight); the
+ * modulation (mod_scale, mod_shift: bf16 [mod_rows, K], row stride ldmod) may
+ * be NULL (plain RMSNorm). normed, if not NULL, receives n (bf16 [M, K], row
+ * stride ldn). x bf16 [M, K] (row stride ldx); y e4m3 [M, K]; y_scale fp32 [M].
+ * Replaces: _pre_ref / the compiled `pre` followed by quantize_rows,
+ *           src/models/ops/fused_block.py:41-44,101-108 and
+ *           src/models/ops/fp8_linear.py:110-117.
+ * Requires: K % 8 == 0, K <= 16384, ldx, ldy, ldn, ldmod multiples of 8 and
+ *           >= K; x, weight, mod_scale, mod_shift, normed 16-byte aligned; y 8-byte.
+ */
+int vdn_fp8_norm_quantize_rows(const void *x, int64_t M, int64_t K, int64_t ldx,
+                               const void *weight, float eps, const void *mod_scale,
+                               const void *mod_shift, int64_t ldmod, const int32_t *mod_index,
+                               int64_t mod_rows, void *y, int64_t ldy, float *y_scale,
+                               void *normed, int64_t ldn, hipStream_t stream);
+
+/*
  * Rowwise weight quantization, optionally after a fused LoRA merge.
  *   W' = W                                        if lora_a == NULL
  *   W' = bf16(W + bf16(lora_scale * (B @ A)))     otherwise (fp32 accumulate)

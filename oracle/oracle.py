@@ -21,6 +21,9 @@ Reference functions restated (paths relative to the reference checkout):
                         tanh approximation of GELU, pinned against torch's
                         F.gelu(approximate="tanh")
   gated                 src/models/ops/fused_block.py:47-49 (_post_ref)
+  norm_quantize_rows    src/models/ops/fused_block.py:41-44 (_pre_ref, as the compiled
+                        `pre` evaluates it: binary32-or-better chain, one bf16 rounding),
+                        then quantize_rows on the bf16 result
 """
 import ctypes
 import os
@@ -212,6 +215,39 @@ def dequant_linear(qx, sx, qw, sw, bias=None, epilogue="none", gate=None, gate_i
     elif epilogue != "none":
         raise ValueError(f"unknown epilogue {epilogue!r}")
     return out
+
+
+def norm_rows(x, weight=None, eps=1e-6, scale=None, shift=None, indices=None, return_terms=False):
+    """RMSNorm + AdaLN affine in float64, rounded once to bf16 (through binary32):
+    n = bf16(x * rsqrt(mean(x^2) + eps) * w * (1 + scale[i]) + shift[i]).
+    x bf16 bits [M, K]; weight bf16 bits [K] or None; scale/shift bf16 bits [T, K] or
+    None; indices [M] (clamped into the table) or None (row 0). Returns bf16 bits, and
+    with return_terms also the magnitude of the affine's two terms, |n - shift| + |shift|
+    (float64), the scale at which a binary32 evaluation of the chain errs."""
+    xv = bf16_decode(_u16(x)).astype(np.float64)
+    M, K = xv.shape
+    rstd = 1.0 / np.sqrt(np.mean(xv * xv, axis=1, keepdims=True) + float(np.float32(eps)))
+    v = xv * rstd
+    if weight is not None:
+        v = v * bf16_decode(_u16(weight)).astype(np.float64).reshape(1, K)
+    if scale is not None:
+        sc = bf16_decode(_u16(scale)).astype(np.float64).reshape(-1, K)
+        sh = bf16_decode(_u16(shift)).astype(np.float64).reshape(-1, K)
+        idx = np.zeros(M, np.int64) if indices is None else np.clip(np.asarray(indices, np.int64), 0, sc.shape[0] - 1)
+        v = v * (1.0 + sc[idx])
+        terms = np.abs(v) + np.abs(sh[idx])
+        v = v + sh[idx]
+    else:
+        terms = np.abs(v)
+    out = bf16_encode(v.astype(np.float32))
+    return (out, terms) if return_terms else out
+
+
+def norm_quantize_rows(x, weight=None, eps=1e-6, scale=None, shift=None, indices=None):
+    """(codes, scales, normed bf16 bits) of the fused pre-norm + quantize_rows."""
+    n = norm_rows(x, weight, eps, scale, shift, indices)
+    q, s = quantize_rows(n)
+    return q, s, n
 
 
 def rel_l2(got, want):

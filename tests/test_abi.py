@@ -56,6 +56,14 @@ FAKE = 1 << 20        # never dereferenced: every call below fails validation fi
     (lambda l: l.vdn_fp8_quantize_rows(None, 4, 8, 8, FAKE, 8, FAKE, None), "null"),
     (lambda l: l.vdn_fp8_quantize_rows(FAKE + 8, 4, 8, 8, FAKE, 8, FAKE, None), "aligned"),
     (lambda l: l.vdn_fp8_swiglu_quantize_rows(FAKE, 4, 8, 8, FAKE, 8, FAKE, None), "2K"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 8, 8, None, 1e-6, FAKE, None, 8, None, 1, FAKE, 8, FAKE,
+                                            None, 8, None), "together"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 8, 8, None, -1.0, None, None, 0, None, 0, FAKE, 8, FAKE,
+                                            None, 8, None), "eps"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 8, 8, FAKE, 1e-6, FAKE, FAKE, 8, None, 0, FAKE, 8, FAKE,
+                                            None, 8, None), "table"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 16392, 16392, None, 1e-6, None, None, 0, None, 0, FAKE,
+                                            16392, FAKE, None, 16392, None), "16384"),
     (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 8, 8, FAKE, None, 4, 1.0, FAKE, 8, FAKE, None, None), "together"),
     (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 32, 32, FAKE, FAKE, 200, 1.0, FAKE, 32, FAKE, None, None), "rank"),
     (lambda l: l.vdn_fp8_requantize_weight(FAKE, 4, 24, 24, FAKE, FAKE, 8, 1.0, FAKE, 24, FAKE, None, None), "K % 16"),
@@ -78,6 +86,8 @@ def test_empty_problems_are_no_ops():
     assert lib.vdn_fp8_quantize_rows(None, 0, 8, 8, None, 8, None, None) == L.OK
     assert lib.vdn_fp8_gemm(None, None, None, None, 0, 16, 32, 32, 32, None, 0, None, None, 0, 0, None, 0, None, 16, None) == L.OK
     assert lib.vdn_fp8_requantize_weight(None, 0, 8, 8, None, None, 0, 1.0, None, 8, None, None, None) == L.OK
+    assert lib.vdn_fp8_norm_quantize_rows(None, 0, 8, 8, None, 1e-6, None, None, 0, None, 0, None, 8, None,
+                                          None, 8, None) == L.OK
 
 
 def test_check_raises_reference_exception_types():

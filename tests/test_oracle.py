@@ -269,3 +269,51 @@ def test_reference_rounding_points():
     assert np.array_equal(ref, O.bf16_decode(O.bf16_encode(ref.astype(np.float32))))   # bf16 values
     assert np.any(ref != single)
     assert O.rel_l2(ref, raw) < 3e-3
+
+
+# ---------------------------------------------------------------------------------
+# the fused pre-norm (RMSNorm + AdaLN affine) feeding the quantizer
+# ---------------------------------------------------------------------------------
+
+def test_norm_rows_matches_torch_rms_norm():
+    """Against torch's own F.rms_norm in float64, then the affine of _pre_ref."""
+    import torch.nn.functional as F
+    rng = np.random.default_rng(21)
+    M, K, T = 37, 320, 3
+    x = O.bf16_encode(rng.standard_normal((M, K), dtype=np.float32) * 2)
+    w = O.bf16_encode(1 + 0.1 * rng.standard_normal(K, dtype=np.float32))
+    sc = O.bf16_encode(0.2 * rng.standard_normal((T, K), dtype=np.float32))
+    sh = O.bf16_encode(0.2 * rng.standard_normal((T, K), dtype=np.float32))
+    idx = rng.integers(0, T, M)
+    got = O.bf16_decode(O.norm_rows(x, w, 1e-6, sc, sh, idx)).astype(np.float64)
+    xt = torch.from_numpy(O.bf16_decode(x).astype(np.float64))
+    ref = F.rms_norm(xt, (K,), torch.from_numpy(O.bf16_decode(w).astype(np.float64)), float(np.float32(1e-6)))
+    it = torch.from_numpy(idx)
+    ref = ref * (1 + torch.from_numpy(O.bf16_decode(sc).astype(np.float64))[it]) \
+        + torch.from_numpy(O.bf16_decode(sh).astype(np.float64))[it]
+    want = ref.to(torch.float32).to(torch.bfloat16).to(torch.float64).numpy()
+    assert np.mean(got == want) > 0.999 and np.max(np.abs(got - want)) <= np.max(np.abs(want)) * 2 ** -7
+
+
+def test_norm_rows_closed_forms():
+    """A constant row normalizes to sign(c) (eps = 0); the affine then applies exactly;
+    with no weight and no table the result is x * rsqrt(mean(x^2) + eps)."""
+    K = 64
+    x = O.bf16_encode(np.array([[3.0] * K, [-0.5] * K], np.float32))
+    w = O.bf16_encode(np.full(K, 2.0, np.float32))
+    sc = O.bf16_encode(np.full((1, K), 0.5, np.float32))
+    sh = O.bf16_encode(np.full((1, K), 0.25, np.float32))
+    n = O.bf16_decode(O.norm_rows(x, w, 0.0, sc, sh))
+    assert np.all(n[0] == 2.0 * 1.5 + 0.25) and np.all(n[1] == -2.0 * 1.5 + 0.25)
+    x2 = O.bf16_encode(np.array([[1.0, -1.0, 2.0, -2.0] * 16], np.float32))
+    n2 = O.bf16_decode(O.norm_rows(x2, None, 0.0))
+    r = 1 / np.sqrt(2.5)
+    assert np.all(n2 == O.bf16_decode(O.bf16_encode((O.bf16_decode(x2) * r).astype(np.float32))))
+
+
+def test_norm_quantize_is_quantize_of_normed():
+    rng = np.random.default_rng(22)
+    x = O.bf16_encode(rng.standard_normal((9, 256), dtype=np.float32))
+    q, s, n = O.norm_quantize_rows(x)
+    q2, s2 = O.quantize_rows(n)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)

@@ -1,6 +1,7 @@
 // Row quantizers for the fp8 linear path (gfx950):
 //   - per-token activation quantization      (vdn_fp8_quantize_rows)
 //   - fused SwiGLU + per-token quantization  (vdn_fp8_swiglu_quantize_rows)
+//   - fused RMSNorm + AdaLN affine + per-token quantization (vdn_fp8_norm_quantize_rows)
 //   - rowwise weight quantization, no LoRA   (vdn_fp8_requantize_weight)
 //
 // All three are HBM-bound: 2 bytes in and 1 byte out per element plus 4 bytes
@@ -196,6 +197,119 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant(
     }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm + AdaLN affine + quantize
+// ---------------------------------------------------------------------------
+
+struct NormArgs {
+    const uint16_t* x;
+    int64_t M, K, ldx;
+    const uint16_t* weight;   // [K] or NULL
+    float eps;
+    const uint16_t* mod_scale;  // [T, K] or NULL (then mod_shift is NULL too)
+    const uint16_t* mod_shift;
+    int64_t ldmod;
+    const int32_t* mod_index;   // [M] or NULL (row 0)
+    int64_t mod_rows;
+    uint8_t* y;
+    int64_t ldy;
+    float* y_scale;
+    uint16_t* normed;           // [M, K] or NULL
+    int64_t ldn;
+};
+
+__device__ __forceinline__ float wave_sum_f32(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// One wave per row, the row in VGPRs:
+//   rstd   = 1 / sqrt(sum_k x^2 / K + eps)                       (binary32)
+//   n[k]   = bf16(((x[k] * rstd) * w[k]) * (1 + scale[i][k]) + shift[i][k])
+//   y, s   = the quantize_rows arithmetic on n
+// with i = mod_index[row] (clamped into the table). The affine chain is held in
+// binary32 and rounded once, as the compiled `pre` of fused_block.py does; the
+// codes follow from the bf16 n exactly as quantize_rows' do.
+template <int CPL>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs p)
+{
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= p.M) return;
+    const int nch = (int)(p.K >> 3);
+    const uint4* xr = reinterpret_cast<const uint4*>(p.x + row * p.ldx);
+
+    uint4 v[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        v[c] = (idx < nch) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = bf16_lo(w4[e]), hi = bf16_hi(w4[e]);
+            ss += lo * lo;
+            ss += hi * hi;
+        }
+    }
+    ss = wave_sum_f32(ss);
+    const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+
+    int64_t ti = 0;
+    if (p.mod_index) ti = min(max((int64_t)p.mod_index[row], (int64_t)0), p.mod_rows - 1);
+    const uint4* wr = reinterpret_cast<const uint4*>(p.weight);
+    const uint4* scr = reinterpret_cast<const uint4*>(p.mod_scale + ti * p.ldmod);
+    const uint4* shr = reinterpret_cast<const uint4*>(p.mod_shift + ti * p.ldmod);
+    uint32_t m2 = 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        if (idx >= nch) continue;
+        const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+        uint4 wv = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // 1.0
+        uint4 sc = make_uint4(0u, 0u, 0u, 0u), sh = sc;
+        if (p.weight) wv = wr[idx];
+        if (p.mod_scale) { sc = scr[idx]; sh = shr[idx]; }
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, sw[4] = {sc.x, sc.y, sc.z, sc.w}, hw[4] = {sh.x, sh.y, sh.z, sh.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float a = (bf16_lo(xw[e]) * rstd) * bf16_lo(ww[e]);
+            float b = (bf16_hi(xw[e]) * rstd) * bf16_hi(ww[e]);
+            if (p.mod_scale) {
+                a = a * (1.0f + bf16_lo(sw[e])) + bf16_lo(hw[e]);
+                b = b * (1.0f + bf16_hi(sw[e])) + bf16_hi(hw[e]);
+            }
+            o[e] = pack_bf16x2(a, b);
+        }
+        v[c] = make_uint4(o[0], o[1], o[2], o[3]);
+        m2 = absmax_bf16x2(m2, v[c].x);
+        m2 = absmax_bf16x2(m2, v[c].y);
+        m2 = absmax_bf16x2(m2, v[c].z);
+        m2 = absmax_bf16x2(m2, v[c].w);
+    }
+    const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
+    if (lane == 0) p.y_scale[row] = scale;
+    const float r = 1.0f / scale;
+    uint2* yr = reinterpret_cast<uint2*>(p.y + row * p.ldy);
+    uint4* nr = reinterpret_cast<uint4*>(p.normed + row * p.ldn);
+    const bool finite = __builtin_isfinite(scale);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + kLanes * c;
+        if (idx >= nch) continue;
+        if (p.normed) nr[idx] = v[c];
+        yr[idx] = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
+    }
+}
+
 template <bool kWeight>
 void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t K,
                      int64_t ldx, uint8_t* y, int64_t ldy, float* s)
@@ -271,6 +385,39 @@ extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K,
         default: return set_error(VDN_FP8_EINVAL, "swiglu_quantize_rows: unsupported K");
     }
     return check_launch("swiglu_quantize_rows");
+}
+
+extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, int64_t ldx, const void* weight,
+                                          float eps, const void* mod_scale, const void* mod_shift, int64_t ldmod,
+                                          const int32_t* mod_index, int64_t mod_rows, void* y, int64_t ldy,
+                                          float* y_scale, void* normed, int64_t ldn, hipStream_t stream)
+{
+    if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: negative shape");
+    if (M == 0) return VDN_FP8_OK;
+    if (K == 0) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: K must be positive");
+    if (!x || !y || !y_scale) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: null pointer");
+    if (!mod_scale != !mod_shift) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: scale and shift go together");
+    if (K % 8 || ldx % 8 || ldy % 8 || ldx < K || ldy < K || (normed && (ldn % 8 || ldn < K)) ||
+        (mod_scale && (ldmod % 8 || ldmod < K || mod_rows < 1)))
+        return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: need K and the row strides multiples of 8 and >= K, "
+                                         "and a modulation table of >= 1 row");
+    if (!(eps >= 0.0f)) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: eps must be >= 0");
+    if (!aligned(x, 16) || !aligned(y, 8) || (weight && !aligned(weight, 16)) || (mod_scale && !aligned(mod_scale, 16)) ||
+        (mod_shift && !aligned(mod_shift, 16)) || (normed && !aligned(normed, 16)) || (mod_index && !aligned(mod_index, 4)))
+        return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: misaligned pointer (x, weight, scale, shift, normed 16 B; y 8 B)");
+    const int64_t nch = K / 8;
+    if (nch > 32 * kLanes) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: K=%lld above the supported 16384", (long long)K);
+    NormArgs p{(const uint16_t*)x, M, K, ldx, (const uint16_t*)weight, eps, (const uint16_t*)mod_scale,
+               (const uint16_t*)mod_shift, ldmod, mod_index, mod_rows, (uint8_t*)y, ldy, y_scale, (uint16_t*)normed, ldn};
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    switch (pick_cpl(nch)) {
+#define VDN_CASE(n) case n: hipLaunchKernelGGL(k_norm_quant<n>, grid, block, 0, stream, p); break;
+        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
+        VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
+#undef VDN_CASE
+        default: return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
+    }
+    return check_launch("norm_quantize_rows");
 }
 
 namespace vdn {

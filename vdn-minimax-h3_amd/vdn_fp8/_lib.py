@@ -21,6 +21,8 @@ _P, _I64, _F32, _I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c
 EXPORTS = (
     ("vdn_fp8_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     ("vdn_fp8_swiglu_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    ("vdn_fp8_norm_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _F32, _P, _P, _I64, _P, _I64, _P, _I64, _P,
+                                          _P, _I64, _P]),
     ("vdn_fp8_requantize_weight", _I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _F32, _P, _I64, _P, _P, _P]),
     ("vdn_fp8_gemm", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
                             _P, _I64, _P, _I64, _P]),
