@@ -260,6 +260,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
     }
     ss = wave_sum_f32(ss);
     const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+    // Opaque to the optimizer: the second sweep unpacks the bf16 pairs again
+    // instead of keeping the first sweep's binary32 copies live (twice the VGPRs).
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) asm volatile("" : "+v"(v[c].x), "+v"(v[c].y), "+v"(v[c].z), "+v"(v[c].w));
 
     int64_t ti = 0;
     if (p.mod_index) ti = min(max((int64_t)p.mod_index[row], (int64_t)0), p.mod_rows - 1);
