@@ -219,6 +219,13 @@ def main():
         ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
         extra["quantize_rows_13824"] = {"ms": round(ms, 4),
                                         "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
+        # SwiGLU + quantize at the H3 FFN width (projection output [M, 2 x 14336])
+        hh = torch.empty(M, 2 * 14336, dtype=torch.bfloat16, device=dev).normal_()
+        ms = _time_region(lambda: vdn_fp8.swiglu_quantize(hh), reps)
+        sw_bytes = M * (2 * 2 * 14336 + 14336 + 4)
+        extra["swiglu_quantize_h3"] = {"shape": [M, 2 * 14336], "ms": round(ms, 4),
+                                       "GB/s": round(sw_bytes / (ms * 1e-3) / 1e9, 1)}
+        del hh
         # the block's pre-norm (RMSNorm + AdaLN affine, table of 2 rows) fused with the quantizer
         g = torch.Generator().manual_seed(6)
         nw = (1 + 0.05 * torch.randn(K, generator=g)).to(torch.bfloat16).to(dev)

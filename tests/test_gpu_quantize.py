@@ -131,7 +131,7 @@ def test_quantize_rows_exhaustive(device):
         _check(x, device)
 
 
-@pytest.mark.parametrize("M,K", [(1, 8), (7, 512), (16, 5120), (5, 7168), (3, 14336)])
+@pytest.mark.parametrize("M,K", [(1, 8), (7, 512), (16, 5120), (5, 7168), (3, 14336), (257, 14336), (9, 6152)])
 def test_swiglu_quantize(device, M, K):
     rng = np.random.default_rng(K + M)
     hb = _randn_bits(rng, M, 2 * K, 2.0)

@@ -314,6 +314,72 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
     }
 }
 
+// Wide rows (K > 8192 in the H3 FFN: 14336): WPR waves share a row, each holding
+// every WPR-th 1 KiB slice of it, so the binary32 activations fit in registers at
+// a useful occupancy; the row maximum is combined through LDS.
+template <int CPL, int WPR>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
+    const uint16_t* __restrict__ h, int64_t M, int64_t K, int64_t ldh,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    static_assert(kWavesPerBlock % WPR == 0, "rows per workgroup");
+    __shared__ uint32_t smax[kWavesPerBlock];
+    const int lane = threadIdx.x & (kLanes - 1), wave = threadIdx.x / kLanes;
+    const int part = wave % WPR;
+    const int64_t row = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
+    const bool valid = row < M;                      // no early return: the barrier below
+    const int nch = (int)(K >> 3);
+    const int64_t r0 = valid ? row : 0;
+    const uint4* ar = reinterpret_cast<const uint4*>(h + r0 * ldh);
+    const uint4* gr = reinterpret_cast<const uint4*>(h + r0 * ldh + K);
+
+    float act[CPL][8];
+    float amax = 0.0f;
+    bool nan_seen = false;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = part * kLanes + lane + kLanes * WPR * c;
+        uint4 a = make_uint4(0u, 0u, 0u, 0u), g = a;
+        if (valid && idx < nch) { a = ar[idx]; g = gr[idx]; }
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            act[c][2 * j] = swiglu(bf16_lo(aw[j]), bf16_lo(gw[j]));
+            act[c][2 * j + 1] = swiglu(bf16_hi(aw[j]), bf16_hi(gw[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            nan_seen |= __builtin_isnan(act[c][j]);
+            amax = fmaxf(amax, fabsf(act[c][j]));
+        }
+    }
+    uint32_t mbits = wave_max_u32(nan_seen ? 0x7fc00000u : __float_as_uint(amax));
+    if (lane == 0) smax[wave] = mbits;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
+    if (!valid) return;
+    const float scale = row_scale(__uint_as_float(mbits));
+    if (part == 0 && lane == 0) scale_out[row] = scale;
+    const float r = 1.0f / scale;
+    const bool finite = __builtin_isfinite(scale);
+    uint2* yr = reinterpret_cast<uint2*>(y + row * ldy);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = part * kLanes + lane + kLanes * WPR * c;
+        if (idx >= nch) continue;
+        float q[8];
+        if (finite) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false, false>(act[c][j], scale, r);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false, true>(act[c][j], scale, r);
+        }
+        yr[idx] = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
+    }
+}
+
 template <bool kWeight>
 void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t K,
                      int64_t ldx, uint8_t* y, int64_t ldy, float* s)
@@ -381,6 +447,14 @@ extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K,
     const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
     const uint16_t* hp = (const uint16_t*)h;
     uint8_t* yp = (uint8_t*)y;
+    if (nch > 12 * kLanes) {            // K > 6144: four waves per row
+        const dim3 g1((unsigned)M);
+        const int cpl = pick_cpl((nch + 3) / 4);
+        if (cpl <= 4) hipLaunchKernelGGL((k_swiglu_quant_split<4, 4>), g1, block, 0, stream, hp, M, K, ldh, yp, ldy, scale);
+        else if (cpl <= 6) hipLaunchKernelGGL((k_swiglu_quant_split<6, 4>), g1, block, 0, stream, hp, M, K, ldh, yp, ldy, scale);
+        else hipLaunchKernelGGL((k_swiglu_quant_split<8, 4>), g1, block, 0, stream, hp, M, K, ldh, yp, ldy, scale);
+        return check_launch("swiglu_quantize_rows");
+    }
     switch (pick_cpl(nch)) {
 #define VDN_CASE(n) case n: hipLaunchKernelGGL(k_swiglu_quant<n>, grid, block, 0, stream, hp, M, K, ldh, yp, ldy, scale); break;
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
