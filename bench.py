@@ -45,6 +45,53 @@ def _gpu_clock():
         return None
 
 
+def _smi_sample():
+    """(mean graphics clock over the XCDs in MHz, socket power in W) from amd-smi, or None."""
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-c", "-p", "--json"], capture_output=True, text=True, timeout=10)
+        d = json.loads(r.stdout)
+        g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
+        clks = [v["clk"]["value"] for k, v in g.get("clock", {}).items()
+                if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+        pw = g.get("power", {}).get("socket_power", {})
+        return (sum(clks) / len(clks) if clks else None, pw.get("value") if isinstance(pw, dict) else None)
+    except Exception:
+        return None
+
+
+def _under_load(fn, seconds=2.0):
+    """Runs fn back to back for about `seconds` while a thread samples amd-smi: the clock the
+    part sustains on this work and the power it draws (the clock falls when the power limit
+    binds)."""
+    import threading
+    import torch
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        time.sleep(0.3)                      # let the clock settle under the load
+        while not stop.is_set():
+            smp = _smi_sample()
+            if smp is None:
+                return
+            samples.append(smp)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    t_end = time.perf_counter() + seconds
+    th.start()
+    while time.perf_counter() < t_end:
+        for _ in range(25):
+            fn()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    clk = [c for c, _ in samples if c]
+    pw = [w for _, w in samples if w]
+    if not clk:
+        return None
+    return {"gfx_mhz": round(sum(clk) / len(clk)), "gfx_mhz_min": round(min(clk)),
+            "socket_w": round(sum(pw) / len(pw)) if pw else None, "samples": len(clk)}
+
+
 def _time_region(fn, reps):
     """Mean ms of fn() over reps launches, from HIP events on the current stream (after one
     untimed call)."""
@@ -216,6 +263,20 @@ def main():
             ms = _time_region(fn, reps)
             tf = wl.linear_flops(M, n_, k_) / (ms * 1e-3) / 1e12
             extra[name] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP8_TFLOPS, 4)}
+        # The QKV GEMM again with every code of X and W set to e4m3 1.0: same instructions, same
+        # memory traffic, but operands that toggle no multiplier bits. The gap to the line above
+        # is what random operands cost in clock (the part holds 2.4 GHz only on such data).
+        lin_u = _make_linear(w_cpu, b_cpu, dev)
+        lin_u.weight_fp8.view(torch.uint8).fill_(0x38)
+        qx0, sx0 = vdn_fp8.quantize_rows(x)
+        qu = torch.full_like(qx0.view(torch.uint8), 0x38).view(qx0.dtype)
+        ms = _time_region(lambda: lin_u.forward_quantized(qu, sx0), reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        extra["gemm_qkv_uniform_codes"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                           "frac": round(tf / PEAK_FP8_TFLOPS, 4),
+                                           "under_load": _under_load(lambda: lin_u.forward_quantized(qu, sx0))}
+        extra["gemm_qkv_under_load"] = _under_load(lambda: lin.forward_quantized(qx0, sx0))
+        del lin_u, qu
         ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
         extra["quantize_rows_13824"] = {"ms": round(ms, 4),
                                         "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
