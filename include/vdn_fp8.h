@@ -104,7 +104,7 @@ int vdn_fp8_norm_quantize_rows(const void *x, int64_t M, int64_t K, int64_t ldx,
  *           src/models/ops/fp8_linear.py:262-267, preceded by the update of
  *           merge_lora_state, src/inference/utils/lora.py:80-94.
  * Requires: K % 8 == 0, ldw % 8 == 0, ldq % 8 == 0; with LoRA: 1 <= rank <= 128,
- *           K % 16 == 0, lora_a 16-byte aligned, wq rows 4-byte aligned. With
+ *           K % 16 == 0, lora_a 16-byte aligned, w_merged 8-byte aligned. With
  *           LoRA and codes, w_scale holds the row maxima between the kernels of
  *           the call (it is the only scratch the call needs).
  */

@@ -85,7 +85,11 @@ def _check_lora(w, a, b, scale, device, max_mismatch=2e-3):
 
 
 @pytest.mark.parametrize("N,K,r", [(16, 256, 64), (40, 1024, 16), (33, 4096, 64), (64, 5120, 128),
-                                   (17, 6144, 32), (20, 8192, 96), (18, 14336, 64), (5, 16384, 8)])
+                                   (17, 6144, 32), (20, 8192, 96), (18, 14336, 64), (5, 16384, 8),
+                                   # odd ranks (2-byte B rows), partial column stripes, one row,
+                                   # partial row tiles
+                                   (24, 2048, 5), (70, 1280, 33), (9, 272, 19), (130, 4112, 64),
+                                   (1, 5120, 64), (200, 768, 127)])
 def test_requant_lora_shapes(device, N, K, r):
     print(f"lora requant N={N} K={K} r={r}", flush=True)
     rng = np.random.default_rng(N + K + r)

@@ -6,26 +6,31 @@
 //
 // The reference merges in place on the bf16 weight (lora.py:91-92) and then
 // quantizes it in eager torch (fp8_linear.py:262-267): several full passes over
-// W plus the write-back of W'. Here W' is never stored unless asked for. The
-// weight is cut into 64-row x 256-column tiles, each a workgroup of four
-// waves (16 rows each), so the work is spread over thousands of independent
-// workgroups:
-//   pass 1 (k_lora_tiles<.., kRowMax>)   W' of the tile in registers, its row
-//                                        maxima merged into w_scale (used as a
-//                                        uint32 max, zeroed first);
-//   pass 2 (k_lora_tiles<.., kQuantize>) W' recomputed (W re-read, mostly from
-//                                        the last-level cache), the codes written;
-//   k_rowmax_to_scale                    w_scale[n] = the reference's scale.
+// W plus the write-back of W'. Here W' is never stored unless asked for.
+//
+// Work split: the weight is cut into 256-column stripes and 64-row tiles. A
+// workgroup (four waves, 16 rows each) owns one stripe and walks a set of its
+// row tiles, so the stripe's slice of A is staged in LDS once per workgroup;
+// the next tile's W and B are loaded into registers while the current tile is
+// computed. Two such passes:
+//   pass 1 (kRowMax)   W + delta in binary32 per element, the row maxima of
+//                      |.| merged into w_scale (used as a uint32 max of bf16
+//                      magnitude bits, zeroed first). Rounding to nearest is
+//                      monotone and symmetric, so max |bf16(x)| = bf16(max |x|):
+//                      the elements are not rounded in this pass.
+//   pass 2 (kQuantize) W' recomputed (W re-read, largely from the last-level
+//                      cache) and the codes written; the workgroups of stripe 0
+//                      turn the row maxima into the reference's scales in place.
 // Merge-only calls (no codes) run pass 2's body with the W' store alone.
 //
-// The rank-r update uses v_mfma_f32_16x16x32_bf16: MFMA row index = k (16
-// columns of W), column index = n (16 rows of W), reduction = rank. Products of
-// bf16 are exact in fp32 and the accumulation is fp32, as the reference's fp32
-// matmul. The MFMA's k-side operand is A transposed, so each workgroup stages
-// A[:, k0 : k0 + 256] in LDS as rows of k (the rank contiguous, rows padded to
-// rank + 8 elements: the 16-row reads and the staging writes are both
-// conflict-free at rank 64). Each lane ends with 4 consecutive k of one row n,
-// so W and W' move 8 bytes per lane and the codes 4 bytes per lane.
+// The rank-r update uses v_mfma_f32_16x16x32_bf16: MFMA row index = a column
+// k of W, column index = a row n, reduction = rank. Products of bf16 are exact
+// in fp32 and the accumulation is fp32, as the reference's fp32 matmul. The
+// MFMA's k-side operand is A transposed, staged in LDS as one row per column
+// k (rank contiguous, padded to rank + 8 elements). The staging permutes the
+// columns (at_row) so that each lane's outputs over four MFMA tiles are 16
+// consecutive columns of one row: W and W' move 32 bytes per lane and group,
+// the codes 16.
 #include <stdint.h>
 
 #include "vdn_common.h"
@@ -36,9 +41,10 @@ namespace {
 constexpr int kRowsPerWave = 16;
 constexpr int kWaves = 4;
 constexpr int kLanes = 64;
+constexpr int kThreads = kWaves * kLanes;
 constexpr int kTileRows = kRowsPerWave * kWaves;   // 64
-constexpr int kTileCols = 256;                      // 16 MFMA tiles of 16 columns
-constexpr int kSub = kTileCols / 16;
+constexpr int kTileCols = 256;                      // one stripe
+constexpr int kGroups = kTileCols / 64;             // per lane: 16 consecutive columns of each 64
 
 enum Mode { kRowMax = 0, kQuantize = 1, kMergeOnly = 2 };
 
@@ -57,12 +63,29 @@ struct Args {
     int64_t ldq;
     float* w_scale;      // pass 1: the row maxima as uint32 bf16 magnitude bits
     uint16_t* w_merged;  // nullable, row stride ldw
+    int wm16;            // w_merged rows are 16-byte aligned
+    int stripes;         // ceil(K / 256); the grid is stripes x (tile walkers per stripe)
+    int row_tiles;       // ceil(N / 64)
 };
 
+// LDS row of column k (0..255) of the stripe: MFMA tile t = 4 (k / 64) +
+// (k % 16) / 4 holds, in its row i = 4 ((k % 64) / 16) + k % 4, column k. Lane
+// (n, g) of tile t gets rows 4 g .. 4 g + 3, so over t = 4 c .. 4 c + 3 it gets
+// columns 64 c + 16 g .. + 15.
+__device__ __forceinline__ int at_row(int k)
+{
+    return 64 * (k >> 6) + 16 * ((k >> 2) & 3) + 4 * ((k >> 4) & 3) + (k & 3);
+}
+
+// Four bf16 values (two packed words) -> four codes: quotient by the bf16 scale,
+// rounded to bf16 (two per conversion; opaque so the pair stays one
+// instruction), then e4m3.
 __device__ __forceinline__ uint32_t codes4(uint2 v, float s, float r)
 {
-    return pack_e4m3x4(round_bf16(div_by_scale(bf16_lo(v.x), s, r)), round_bf16(div_by_scale(bf16_hi(v.x), s, r)),
-                       round_bf16(div_by_scale(bf16_lo(v.y), s, r)), round_bf16(div_by_scale(bf16_hi(v.y), s, r)));
+    uint32_t q01 = pack_bf16x2(div_by_scale(bf16_lo(v.x), s, r), div_by_scale(bf16_hi(v.x), s, r));
+    uint32_t q23 = pack_bf16x2(div_by_scale(bf16_lo(v.y), s, r), div_by_scale(bf16_hi(v.y), s, r));
+    asm volatile("" : "+v"(q01), "+v"(q23));
+    return pack_e4m3x4(bf16_lo(q01), bf16_hi(q01), bf16_lo(q23), bf16_hi(q23));
 }
 
 __device__ __forceinline__ uint32_t codes4_exact(uint2 v, float s)
@@ -71,139 +94,247 @@ __device__ __forceinline__ uint32_t codes4_exact(uint2 v, float s)
                        round_bf16(bf16_lo(v.y) / s), round_bf16(bf16_hi(v.y) / s));
 }
 
-// RP = rank padded to a multiple of 32.
-template <int RP, int MODE>
-__global__ __launch_bounds__(kWaves * kLanes) void k_lora_tiles(Args p)
+// Registers of one row tile: W (per group c, 16 columns in two 16-byte
+// pieces), the B operand, and (pass 2) the row-maximum bits.
+template <int RP>
+struct TileRegs {
+    uint4 w[2 * kGroups];
+    bf16x8_t b[RP / 32];
+    uint32_t mbits;
+};
+
+// B operand of rank step s for row nr of the tile based at row n0: lane holds
+// B[n][32 s + 8 g .. +7] (zero beyond the rank), from 2-byte loads (any rank).
+template <int RP>
+__device__ __forceinline__ bf16x8_t b_operand_scalar(const Args& p, __amdgpu_buffer_rsrc_t br, int nr, int s, int g)
 {
-    constexpr int kS = RP + 8;                       // LDS row (one k) in elements
+    const int j0 = 32 * s + 8 * g;
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)((nr * p.rank + j0 + 2 * i) * 2), 0, 0);
+        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)((nr * p.rank + j0 + 2 * i + 1) * 2), 0, 0);
+        e[i] = (lo & 0xffffu) | (hi << 16);
+        const int j = j0 + 2 * i;
+        if (j >= p.rank) e[i] = 0u;
+        else if (j + 1 >= p.rank) e[i] &= 0xffffu;
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(e[0], e[1], e[2], e[3]));
+}
+
+// RP = rank padded to a multiple of 32. BVEC: rows of B 16-byte aligned and
+// rank % 8 == 0, so B is prefetched with the tile's W by 16-byte loads.
+template <int RP, int MODE, bool BVEC>
+__global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
+{
+    constexpr int kS = RP + 8;                       // LDS row (one column k) in elements
     __shared__ __attribute__((aligned(16))) uint16_t sAT[kTileCols * kS];
 
     const int tid = threadIdx.x, lane = tid & (kLanes - 1);
     const int wave = tid / kLanes;
     const int nl = lane & 15, g = lane >> 4;
-    const int64_t k0 = (int64_t)blockIdx.x * kTileCols;
-    const int64_t n = (int64_t)blockIdx.y * kTileRows + wave * kRowsPerWave + nl;
-    const bool nvalid = n < p.N;
+    const int stripe = (int)(blockIdx.x % (unsigned)p.stripes);
+    const int rstep = (int)(gridDim.x / (unsigned)p.stripes);
+    const int64_t k0 = (int64_t)stripe * kTileCols;
+    const int nr = wave * kRowsPerWave + nl;            // row within a tile
 
     // All loads go through buffer descriptors: rows past N and rank rows past
     // the LoRA rank read as zeros with no branch, so the loads stay in flight
-    // together (a load under a divergent branch makes the compiler wait for it).
-    // Columns past K may read the next row's data; they only feed outputs that
-    // are never stored.
-    const int64_t n0 = (int64_t)blockIdx.y * kTileRows;
-    const int64_t rows = min(p.N - n0, (int64_t)kTileRows);
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.w + n0 * p.ldw), 0, (int)(rows * p.ldw * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.b + n0 * p.rank), 0, (int)(rows * p.rank * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)p.a, 0, (int)(p.rank * p.K * 2), 0x00020000);
-    const int nr = wave * kRowsPerWave + nl;            // row within the tile
+    // together. Columns past K may read the next row's data; they only feed
+    // outputs that are neither stored nor counted in a maximum.
+    // A tile past the last one gets empty descriptors (every load reads zero
+    // and touches no memory): the loads stay unconditional, so the compiler
+    // counts them exactly and waits for a tile's loads only where it is used.
+    auto load_tile = [&](int rt, TileRegs<RP>& t) {
+        const int rtc = min(rt, p.row_tiles - 1);
+        const int64_t n0 = (int64_t)rtc * kTileRows;
+        const int64_t rows = rt < p.row_tiles ? min(p.N - n0, (int64_t)kTileRows) : 0;
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.w + n0 * p.ldw), 0, (int)(rows * p.ldw * 2), 0x00020000);
+#pragma unroll
+        for (int c = 0; c < kGroups; ++c) {
+            const uint32_t off = (uint32_t)((nr * p.ldw + k0 + 64 * c + 16 * g) * 2);
+            t.w[2 * c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+            t.w[2 * c + 1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16, 0, 0));
+        }
+        // B operand, raw (the rank mask applies when it is used, so that no
+        // wait for these loads lands here)
+        if (BVEC) {
+            const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.b + n0 * p.rank), 0, (int)(rows * p.rank * 2), 0x00020000);
+#pragma unroll
+            for (int s = 0; s < RP / 32; ++s)
+                t.b[s] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                    br, (uint32_t)((nr * p.rank + 32 * s + 8 * g) * 2), 0, 0));
+        }
+        t.mbits = 0u;
+        if (MODE == kQuantize) {
+            const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.w_scale + n0), 0, (int)(rows * 4), 0x00020000);
+            t.mbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)(nr * 4), 0, 0);
+        }
+    };
 
-    // This lane's W values: row n, columns k0 + 16 t + 4 g .. +3 (K % 16 == 0,
-    // so a 16-column tile is wholly inside or outside the matrix).
-    uint2 w4[kSub];
+    // Stage A^T of the stripe: unit u covers rank rows j = 2 pr, 2 pr + 1 and
+    // columns 8 kg .. 8 kg + 7; each column's pair is one dword at LDS row
+    // at_row(column), element j. Rank rows past the rank read as zeros.
+    {
+        const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)p.a, 0, (int)(p.rank * p.K * 2), 0x00020000);
+        constexpr int kPairs = RP / 2, kUnits = kPairs * (kTileCols / 8);
+        uint4 alo[kUnits / kThreads], ahi[kUnits / kThreads];
 #pragma unroll
-    for (int t = 0; t < kSub; ++t) {
-        const uint32_t off = (uint32_t)((nr * p.ldw + k0 + 16 * t + 4 * g) * 2);
-        w4[t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, off, 0, 0));
-    }
-    // B operand: lane holds B[n][32 s + 8 g .. +7], zero beyond the rank.
-    bf16x8_t bop[RP / 32];
+        for (int i = 0; i < kUnits / kThreads; ++i) {
+            const int u = tid + i * kThreads;
+            const int pr = u % kPairs, kg = u / kPairs;
+            const int64_t j = 2 * pr, k = k0 + 8 * kg;
+            alo[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, (uint32_t)((j * p.K + k) * 2), 0, 0));
+            ahi[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, (uint32_t)(((j + 1) * p.K + k) * 2), 0, 0));
+        }
 #pragma unroll
-    for (int s = 0; s < RP / 32; ++s) {
-        const int j0 = 32 * s + 8 * g;
-        uint32_t e[4];
-        if (p.b_vec) {
-            const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                br, (uint32_t)((nr * p.rank + j0) * 2), 0, 0));
-            e[0] = v.x; e[1] = v.y; e[2] = v.z; e[3] = v.w;
-        } else {
+        for (int i = 0; i < kUnits / kThreads; ++i) {
+            const int u = tid + i * kThreads;
+            const int pr = u % kPairs, kg = u / kPairs;
+            const uint32_t l[4] = {alo[i].x, alo[i].y, alo[i].z, alo[i].w}, h[4] = {ahi[i].x, ahi[i].y, ahi[i].z, ahi[i].w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)((nr * p.rank + j0 + 2 * i) * 2), 0, 0);
-                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)((nr * p.rank + j0 + 2 * i + 1) * 2), 0, 0);
-                e[i] = (lo & 0xffffu) | (hi << 16);
+            for (int e = 0; e < 4; ++e) {
+                uint32_t* d0 = reinterpret_cast<uint32_t*>(sAT + at_row(8 * kg + 2 * e) * kS + 2 * pr);
+                uint32_t* d1 = reinterpret_cast<uint32_t*>(sAT + at_row(8 * kg + 2 * e + 1) * kS + 2 * pr);
+                *d0 = (l[e] & 0xffffu) | (h[e] << 16);
+                *d1 = (l[e] >> 16) | (h[e] & 0xffff0000u);
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = j0 + 2 * i;
-            if (j >= p.rank) e[i] = 0u;
-            else if (j + 1 >= p.rank) e[i] &= 0xffffu;
-        }
-        bop[s] = __builtin_bit_cast(bf16x8_t, make_uint4(e[0], e[1], e[2], e[3]));
     }
-    // Stage A^T: unit u covers rows j = 2p, 2p+1 and columns 8 kg .. 8 kg + 7;
-    // the pair is written as one dword per column at sAT[k][j]. Rows past the
-    // rank read as zeros.
-    constexpr int kPairs = RP / 2, kUnits = kPairs * (kTileCols / 8);
-    uint4 alo[kUnits / (kWaves * kLanes)], ahi[kUnits / (kWaves * kLanes)];
-#pragma unroll
-    for (int i = 0; i < kUnits / (kWaves * kLanes); ++i) {
-        const int u = tid + i * kWaves * kLanes;
-        const int pr = u % kPairs, kg = u / kPairs;
-        const int64_t j = 2 * pr, k = k0 + 8 * kg;
-        alo[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, (uint32_t)((j * p.K + k) * 2), 0, 0));
-        ahi[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ar, (uint32_t)(((j + 1) * p.K + k) * 2), 0, 0));
-    }
-#pragma unroll
-    for (int i = 0; i < kUnits / (kWaves * kLanes); ++i) {
-        const int u = tid + i * kWaves * kLanes;
-        const int pr = u % kPairs, kg = u / kPairs;
-        const uint32_t l[4] = {alo[i].x, alo[i].y, alo[i].z, alo[i].w}, h[4] = {ahi[i].x, ahi[i].y, ahi[i].z, ahi[i].w};
-        uint32_t* dst = reinterpret_cast<uint32_t*>(sAT + (8 * kg) * kS + 2 * pr);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            dst[(2 * e) * (kS / 2)] = (l[e] & 0xffffu) | (h[e] << 16);
-            dst[(2 * e + 1) * (kS / 2)] = (l[e] >> 16) | (h[e] & 0xffff0000u);
-        }
-    }
-    __syncthreads();
 
-    float sb = 0.0f, r = 0.0f;
-    bool finite = true;
-    if (MODE == kQuantize && nvalid) {
-        const uint32_t mbits = reinterpret_cast<const uint32_t*>(p.w_scale)[n];
-        sb = round_bf16(row_scale(bf16_to_f32((uint16_t)mbits)));
-        r = 1.0f / sb;
-        finite = __builtin_isfinite(sb);
-    }
-    uint32_t m2 = 0;
+    auto compute = [&](int rt, const TileRegs<RP>& t) {
+        const int64_t n = (int64_t)rt * kTileRows + nr;
+        const bool nvalid = n < p.N;
+        // B operand: lane holds B[n][32 s + 8 g .. +7], zero beyond the rank
+        // (rank % 8 == 0 on the vector path: all 8 or none)
+        bf16x8_t bop[RP / 32];
+        if (BVEC) {
 #pragma unroll
-    for (int t = 0; t < kSub; ++t) {
-        const int64_t k = k0 + 16 * t + 4 * g;
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        const uint16_t* arow = sAT + (16 * t + nl) * kS + 8 * g;
+            for (int s = 0; s < RP / 32; ++s)
+                bop[s] = (32 * s + 8 * g < p.rank) ? t.b[s] : bf16x8_t{};
+        } else {
+            const int64_t n0 = (int64_t)rt * kTileRows;
+            const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.b + n0 * p.rank), 0, (int)(min(p.N - n0, (int64_t)kTileRows) * p.rank * 2), 0x00020000);
 #pragma unroll
-        for (int s = 0; s < RP / 32; ++s) {
-            const bf16x8_t aop = *reinterpret_cast<const bf16x8_t*>(arow + 32 * s);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[s], acc, 0, 0, 0);
+            for (int s = 0; s < RP / 32; ++s) bop[s] = b_operand_scalar<RP>(p, br, nr, s, g);
         }
-        // delta.to(bf16), then the bf16 add: binary32 add of the two bf16 values, rounded.
-        const float d0 = round_bf16(acc[0] * p.lora_scale), d1 = round_bf16(acc[1] * p.lora_scale);
-        const float d2 = round_bf16(acc[2] * p.lora_scale), d3 = round_bf16(acc[3] * p.lora_scale);
-        uint2 wm;
-        wm.x = pack_bf16x2(bf16_lo(w4[t].x) + d0, bf16_hi(w4[t].x) + d1);
-        wm.y = pack_bf16x2(bf16_lo(w4[t].y) + d2, bf16_hi(w4[t].y) + d3);
-        const bool in = nvalid && k < p.K;
+        float sb = 0.0f, r = 0.0f;
+        bool finite = true;
+        if (MODE == kQuantize) {
+            // w_scale[n] holds either the row maximum's bf16 magnitude bits (below
+            // 2^16) or, once a workgroup of stripe 0 has passed, the reference's
+            // scale (binary32 bits of a value >= 1e-12 or NaN: above 2^16). Both
+            // give the same scale; stripe 0 stores it, so racing readers agree.
+            const float s32 = t.mbits < 0x10000u ? row_scale(bf16_to_f32((uint16_t)t.mbits)) : __uint_as_float(t.mbits);
+            if (stripe == 0 && g == 0 && nvalid) p.w_scale[n] = s32;
+            sb = round_bf16(s32);
+            r = 1.0f / sb;
+            finite = __builtin_isfinite(sb);
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kGroups; ++c) {
+            const int64_t k = k0 + 64 * c + 16 * g;       // this lane's 16 columns k .. k + 15
+            const bool in = nvalid && k < p.K;            // K % 16 == 0: all 16 or none
+            f32x4_t acc[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                const uint16_t* arow = sAT + (16 * (4 * c + m) + nl) * kS + 8 * g;
+#pragma unroll
+                for (int s = 0; s < RP / 32; ++s) {
+                    const bf16x8_t aop = *reinterpret_cast<const bf16x8_t*>(arow + 32 * s);
+                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[s], acc[m], 0, 0, 0);
+                }
+            }
+            // column 16 g + 4 m + e of the group <-> acc[m][e]; W word (m % 2) * 2 + e / 2
+            // of piece m / 2, half e % 2
+            float x[16];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint4 wp = t.w[2 * c + m / 2];
+                const uint32_t ww[4] = {wp.x, wp.y, wp.z, wp.w};
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const uint32_t word = ww[(m % 2) * 2 + e / 2];
+                    // delta.to(bf16) (two at a time), then the bf16 add: binary32 sum
+                    // of the two bf16 values
+                    uint32_t d = pack_bf16x2(acc[m][e] * p.lora_scale, acc[m][e + 1] * p.lora_scale);
+                    // opaque: the compiler would otherwise split the pair back into
+                    // two one-value conversions
+                    asm volatile("" : "+v"(d));
+                    x[4 * m + e] = bf16_lo(word) + bf16_lo(d);
+                    x[4 * m + e + 1] = bf16_hi(word) + bf16_hi(d);
+                }
+            }
+            if (MODE == kRowMax) {
+                float gm = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) gm = __builtin_elementwise_maximum(gm, __builtin_fabsf(x[i]));
+                if (in) mx = __builtin_elementwise_maximum(mx, gm);
+            } else {
+                uint32_t wm[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    wm[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+                    asm volatile("" : "+v"(wm[i]));
+                }
+                if (in && p.w_merged) {
+                    uint16_t* dst = p.w_merged + n * p.ldw + k;
+                    if (p.wm16) {
+                        reinterpret_cast<uint4*>(dst)[0] = make_uint4(wm[0], wm[1], wm[2], wm[3]);
+                        reinterpret_cast<uint4*>(dst)[1] = make_uint4(wm[4], wm[5], wm[6], wm[7]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) reinterpret_cast<uint2*>(dst)[i] = make_uint2(wm[2 * i], wm[2 * i + 1]);
+                    }
+                }
+                if (MODE == kQuantize && in) {
+                    uint32_t q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint2 v = make_uint2(wm[2 * i], wm[2 * i + 1]);
+                        q[i] = finite ? codes4(v, sb, r) : codes4_exact(v, sb);
+                    }
+                    uint2* dq = reinterpret_cast<uint2*>(p.wq + n * p.ldq + k);
+                    dq[0] = make_uint2(q[0], q[1]);
+                    dq[1] = make_uint2(q[2], q[3]);
+                }
+            }
+        }
         if (MODE == kRowMax) {
-            if (in) {
-                m2 = absmax_bf16x2(m2, wm.x);
-                m2 = absmax_bf16x2(m2, wm.y);
-            }
-        } else {
-            if (in && p.w_merged) *reinterpret_cast<uint2*>(p.w_merged + n * p.ldw + k) = wm;
-            if (MODE == kQuantize && in)
-                *reinterpret_cast<uint32_t*>(p.wq + n * p.ldq + k) = finite ? codes4(wm, sb, r) : codes4_exact(wm, sb);
+            // the lanes sharing n differ in g (lane bits 4, 5)
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
+            const uint32_t m = (pack_bf16x2(mx, 0.0f) & 0x7fffu);
+            if (g == 0 && nvalid) atomicMax(reinterpret_cast<uint32_t*>(p.w_scale) + n, m);
         }
-    }
-    if (MODE == kRowMax) {
-        // the lanes sharing n differ in g (lane bits 4, 5)
-        uint32_t m = max(m2 & 0xffffu, m2 >> 16);
-        m = max(m, (uint32_t)__shfl_xor((int)m, 16, 64));
-        m = max(m, (uint32_t)__shfl_xor((int)m, 32, 64));
-        if (g == 0 && nvalid) atomicMax(reinterpret_cast<uint32_t*>(p.w_scale) + n, m);
+    };
+
+    // Walk row tiles rt0, rt0 + rstep, ..., loading each tile's registers one
+    // tile ahead (two register sets, alternating).
+    int rt = (int)(blockIdx.x / (unsigned)p.stripes);
+    TileRegs<RP> ta, tb;
+    load_tile(rt, ta);
+    __syncthreads();                                   // A^T staged
+    while (rt < p.row_tiles) {
+        const int r1 = rt + rstep;
+        load_tile(r1, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rt, ta);
+        __builtin_amdgcn_sched_barrier(0);
+        if (r1 >= p.row_tiles) break;
+        const int r2 = r1 + rstep;
+        load_tile(r2, ta);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(r1, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        rt = r2;
     }
 }
 
@@ -213,30 +344,56 @@ __global__ void k_zero_u32(uint32_t* x, int64_t n)
     if (i < n) x[i] = 0u;
 }
 
-// The row maxima (bf16 magnitude bits) -> the reference's fp32 scale, in place.
-__global__ void k_rowmax_to_scale(float* w_scale, int64_t n)
+// Workgroups of one kernel that fit on a CU at once (cached per kernel).
+template <int RP, int MODE, bool BVEC>
+int resident_per_cu()
 {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) {
-        const uint32_t m = reinterpret_cast<const uint32_t*>(w_scale)[i];
-        w_scale[i] = row_scale(bf16_to_f32((uint16_t)m));
-    }
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&k_lora_stripes<RP, MODE, BVEC>),
+                                                     kThreads, 0) != hipSuccess || nb < 1)
+        nb = 1;
+    cached = nb;
+    return nb;
 }
 
-template <int RP>
-void launch_rp(const Args& p, bool merge_only, hipStream_t st)
+// Grid: stripes x walkers, walkers per stripe chosen so that every workgroup is
+// resident at once (no second wave of workgroups) and no walker is idle.
+template <int RP, int MODE, bool BVEC>
+dim3 stripe_grid(const Args& p, int cus)
 {
-    const dim3 grid((unsigned)((p.K + kTileCols - 1) / kTileCols), (unsigned)((p.N + kTileRows - 1) / kTileRows));
-    const dim3 block(kWaves * kLanes);
+    const int64_t slots = (int64_t)cus * resident_per_cu<RP, MODE, BVEC>();
+    const int64_t walkers = max((int64_t)1, min((int64_t)p.row_tiles, slots / p.stripes));
+    return dim3((unsigned)(walkers * p.stripes));
+}
+
+template <int RP, bool BVEC>
+void launch_rp(const Args& p, bool merge_only, int cus, hipStream_t st)
+{
+    const dim3 block(kThreads);
     if (merge_only) {
-        hipLaunchKernelGGL((k_lora_tiles<RP, kMergeOnly>), grid, block, 0, st, p);
+        const dim3 gm = stripe_grid<RP, kMergeOnly, BVEC>(p, cus);
+        hipLaunchKernelGGL((k_lora_stripes<RP, kMergeOnly, BVEC>), gm, block, 0, st, p);
         return;
     }
     const dim3 vgrid((unsigned)((p.N + 255) / 256)), vblock(256);
+    const dim3 g1 = stripe_grid<RP, kRowMax, BVEC>(p, cus), g2 = stripe_grid<RP, kQuantize, BVEC>(p, cus);
     hipLaunchKernelGGL(k_zero_u32, vgrid, vblock, 0, st, reinterpret_cast<uint32_t*>(p.w_scale), p.N);
-    hipLaunchKernelGGL((k_lora_tiles<RP, kRowMax>), grid, block, 0, st, p);
-    hipLaunchKernelGGL((k_lora_tiles<RP, kQuantize>), grid, block, 0, st, p);
-    hipLaunchKernelGGL(k_rowmax_to_scale, vgrid, vblock, 0, st, p.w_scale, p.N);
+    hipLaunchKernelGGL((k_lora_stripes<RP, kRowMax, BVEC>), g1, block, 0, st, p);
+    hipLaunchKernelGGL((k_lora_stripes<RP, kQuantize, BVEC>), g2, block, 0, st, p);
+}
+
+int device_cus_lora()
+{
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cached[dev] = n;
+    return n;
 }
 
 }  // namespace
@@ -251,22 +408,33 @@ int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, co
     if ((uintptr_t)a % 16) return set_error(VDN_FP8_EINVAL, "requantize_weight: lora_a must be 16-byte aligned");
     if ((uintptr_t)b % 2) return set_error(VDN_FP8_EINVAL, "requantize_weight: lora_b must be 2-byte aligned");
     if (w_merged && ((uintptr_t)w_merged % 8)) return set_error(VDN_FP8_EINVAL, "requantize_weight: w_merged must be 8-byte aligned");
-    if (wq && (((uintptr_t)wq % 4) || (ldq % 4))) return set_error(VDN_FP8_EINVAL, "requantize_weight: wq rows must be 4-byte aligned");
+    if (wq && (((uintptr_t)wq % 8) || (ldq % 8))) return set_error(VDN_FP8_EINVAL, "requantize_weight: wq rows must be 8-byte aligned");
     if (w_scale && ((uintptr_t)w_scale % 4)) return set_error(VDN_FP8_EINVAL, "requantize_weight: w_scale must be 4-byte aligned");
     if ((int64_t)kTileRows * ldw * 2 > 0x7fffffffLL || (rank + 33) * K * 2 > 0x7fffffffLL)
         return set_error(VDN_FP8_EINVAL, "requantize_weight: rows too long for the LoRA path");
-    if ((N + kTileRows - 1) / kTileRows > 65535)
-        return set_error(VDN_FP8_EINVAL, "requantize_weight: N=%lld above the LoRA path's 4194240 rows", (long long)N);
+    if ((N + kTileRows - 1) / kTileRows > (1 << 24) || (K + kTileCols - 1) / kTileCols > (1 << 16))
+        return set_error(VDN_FP8_EINVAL, "requantize_weight: shape [%lld, %lld] too large for the LoRA path",
+                         (long long)N, (long long)K);
     const bool merge_only = wq == nullptr;
     const int b_vec = (rank % 8 == 0) && ((uintptr_t)b % 16 == 0);
-    Args p{w, N, K, ldw, a, b, rank, b_vec, lora_scale, wq, ldq, w_scale, w_merged};
+    const int wm16 = w_merged && ((uintptr_t)w_merged % 16 == 0);
+    const int cus = device_cus_lora();
+    if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "requantize_weight: cannot query the device's compute units");
+    Args p{w, N, K, ldw, a, b, rank, b_vec, lora_scale, wq, ldq, w_scale, w_merged, wm16,
+           (int)((K + kTileCols - 1) / kTileCols), (int)((N + kTileRows - 1) / kTileRows)};
     const int rp = (int)((rank + 31) / 32) * 32;
+#define VDN_LORA_RP(R)                                                      \
+    do {                                                                    \
+        if (b_vec) launch_rp<R, true>(p, merge_only, cus, stream);          \
+        else launch_rp<R, false>(p, merge_only, cus, stream);               \
+    } while (0)
     switch (rp) {
-        case 32: launch_rp<32>(p, merge_only, stream); break;
-        case 64: launch_rp<64>(p, merge_only, stream); break;
-        case 96: launch_rp<96>(p, merge_only, stream); break;
-        default: launch_rp<128>(p, merge_only, stream); break;
+        case 32: VDN_LORA_RP(32); break;
+        case 64: VDN_LORA_RP(64); break;
+        case 96: VDN_LORA_RP(96); break;
+        default: VDN_LORA_RP(128); break;
     }
+#undef VDN_LORA_RP
     return check_launch("requantize_weight (LoRA)");
 }
 

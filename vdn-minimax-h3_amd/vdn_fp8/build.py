@@ -31,6 +31,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions. The LoRA kernels read every MFMA result with VALU code:
+# accumulating in VGPRs (rather than AGPRs) saves one copy per element.
+EXTRA_FLAGS = {"lora_requant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc():
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -44,7 +49,8 @@ def build(verbose=False):
     with tempfile.TemporaryDirectory(prefix="vdnfp8_build_") as tmp:
         def compile_one(src):
             obj = os.path.join(tmp, os.path.splitext(src)[0] + ".o")
-            cmd = [cc, *HIPCC_FLAGS, "-I", _INCLUDE, "-I", _CSRC, "-c", os.path.join(_CSRC, src), "-o", obj]
+            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-I", _INCLUDE, "-I", _CSRC, "-c",
+                   os.path.join(_CSRC, src), "-o", obj]
             r = subprocess.run(cmd, capture_output=True, text=True)
             if r.returncode != 0:
                 raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
