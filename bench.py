@@ -296,6 +296,18 @@ def main():
         ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
         extra["pre_norm_quantize"] = {"ms": round(ms, 4),
                                       "GB/s": round(wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9, 1)}
+        # QK-norm + rope on q of the QKV output (40 heads of 128, a strided view of the fused
+        # [M, 3 x 5120] projection output), fp32 cos/sin tables [M, 128]
+        qkv_out = lin.forward_quantized(*vdn_fp8.quantize_rows(x))
+        qv = qkv_out[:, :5120].unflatten(-1, (40, 128))
+        nq = (1 + 0.05 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+        th = torch.rand(M, 64, device=dev) * 6.28
+        cs, sn = torch.cat([th.cos(), th.cos()], 1), torch.cat([th.sin(), th.sin()], 1)
+        ms = _time_region(lambda: vdn_fp8.qk_prep(qv, nq, 1e-6, cs, sn), reps)
+        qk_bytes = M * 5120 * 2 * 2 + 2 * M * 128 * 4
+        extra["qk_prep_q"] = {"shape": [M, 40, 128], "ms": round(ms, 4),
+                              "GB/s": round(qk_bytes / (ms * 1e-3) / 1e9, 1)}
+        del qkv_out, qv
         extra["gpu_clock"] = _gpu_clock()
     line["extra"] = extra
     if not args.no_cpu_baseline:

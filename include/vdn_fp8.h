@@ -142,6 +142,33 @@ int vdn_fp8_gemm(const void *xq, const float *x_scale, const void *wq, const flo
                  int64_t gate_rows, int64_t ldgate, const void *residual, int64_t ldres,
                  void *out, int64_t ldo, hipStream_t stream);
 
+/*
+ * QK preparation between the q (or k) projection and attention: per-head
+ * RMSNorm, then rotary embedding, in one pass.
+ *   rstd   = 1 / sqrt(sum_i x[t][h][i]^2 / d + eps)                (binary32)
+ *   n[i]   = (x[t][h][i] * rstd) * weight[i]            (weight NULL: no factor)
+ *   c, s   = bf16(cos[t][i]), bf16(sin[t][i])           (i < rotary_dim = R)
+ *   out[t][h][i] = bf16(n[i] c[i] - n[i + R/2] s[i])    for i < R/2
+ *                = bf16(n[i] c[i] + n[i - R/2] s[i])    for R/2 <= i < R
+ *                = bf16(n[i])                           for i >= R
+ * binary32 throughout with one rounding at the store, as the compiled kernel
+ * of the reference (not bitwise with its eager chain, which rounds per op).
+ * x bf16 [T, H, d] (token row stride ldx, heads contiguous), out bf16 likewise
+ * (row stride ldo); weight bf16 [d] or NULL; cos, sin [T, R] (row stride ldcs),
+ * binary32 (cs_bf16 = 0) or bf16 (cs_bf16 = 1); R = 0 means no rotation (cos
+ * and sin may then be NULL).
+ * Replaces: _qk_prep / _qk_prep_body and _rope_body,
+ *           src/models/softmax_attention/kernels.py:8-45, as called from
+ *           HybridAttention._qkv, src/models/hybrid_attention.py:128-130.
+ * Requires: d in {64, 128, 256}; H * d <= 16384; R % 16 == 0 and R <= d;
+ *           ldx, ldo multiples of 8 and >= H * d; x, out, weight, cos, sin
+ *           16-byte aligned and table rows 16-byte multiples.
+ */
+int vdn_fp8_qk_prep(const void *x, int64_t T, int64_t H, int64_t d, int64_t ldx,
+                    const void *weight, float eps, const void *cos, const void *sin,
+                    int64_t rotary_dim, int64_t ldcs, int cs_bf16, void *out, int64_t ldo,
+                    hipStream_t stream);
+
 /* The message of the last failed call on this host thread ("" if none). */
 const char *vdn_fp8_last_error(void);
 

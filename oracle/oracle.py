@@ -24,6 +24,10 @@ Reference functions restated (paths relative to the reference checkout):
   norm_quantize_rows    src/models/ops/fused_block.py:41-44 (_pre_ref, as the compiled
                         `pre` evaluates it: binary32-or-better chain, one bf16 rounding),
                         then quantize_rows on the bf16 result
+  qk_prep               src/models/softmax_attention/kernels.py:8-45 (_qk_prep: per-head
+                        RMSNorm, then the half-split rotary embedding of _rope_body, as
+                        the compiled kernel evaluates it: cos/sin rounded to bf16, the
+                        rest binary32-or-better, one bf16 rounding at the end)
 """
 import ctypes
 import os
@@ -248,6 +252,36 @@ def norm_quantize_rows(x, weight=None, eps=1e-6, scale=None, shift=None, indices
     n = norm_rows(x, weight, eps, scale, shift, indices)
     q, s = quantize_rows(n)
     return q, s, n
+
+
+def qk_prep(x, weight=None, eps=1e-6, cos=None, sin=None, return_terms=False):
+    """QK-norm + rope of one projection in float64, rounded once to bf16 (through
+    binary32). x bf16 bits [T, H, d]; weight bf16 bits [d] or None; cos/sin [T, R]
+    float32 values (rounded to bf16 here, as `cos.to(x.dtype)`) or bf16 bits (uint16),
+    or None. Returns bf16 bits [T, H, d], and with return_terms the magnitude of the
+    rotation's two products |n c| + |r s| (float64), the scale at which a binary32
+    evaluation errs."""
+    xv = bf16_decode(_u16(x)).astype(np.float64)
+    T, H, d = xv.shape
+    rstd = 1.0 / np.sqrt(np.mean(xv * xv, axis=2, keepdims=True) + float(np.float32(eps)))
+    n = xv * rstd
+    if weight is not None:
+        n = n * bf16_decode(_u16(weight)).astype(np.float64).reshape(1, 1, d)
+    terms = np.abs(n)
+    out = n.copy()
+    if cos is not None:
+        def table(t):
+            t = np.asarray(t)
+            bits = t if t.dtype == np.uint16 else bf16_encode(t.astype(np.float32))
+            return bf16_decode(bits).astype(np.float64)[:, None, :]
+        c, s = table(cos), table(sin)
+        R = c.shape[-1]
+        h = R // 2
+        rot = np.concatenate([-n[..., h:R], n[..., :h]], axis=-1)
+        out[..., :R] = n[..., :R] * c + rot * s
+        terms[..., :R] = np.abs(n[..., :R] * c) + np.abs(rot * s)
+    out = bf16_encode(out.astype(np.float32))
+    return (out, terms) if return_terms else out
 
 
 def rel_l2(got, want):

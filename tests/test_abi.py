@@ -20,7 +20,8 @@ def declared_symbols():
 def test_header_declares_the_abi():
     names = declared_symbols()
     assert {"vdn_fp8_quantize_rows", "vdn_fp8_swiglu_quantize_rows", "vdn_fp8_requantize_weight",
-            "vdn_fp8_gemm", "vdn_fp8_last_error", "vdn_fp8_abi_version"} <= set(names)
+            "vdn_fp8_gemm", "vdn_fp8_norm_quantize_rows", "vdn_fp8_qk_prep", "vdn_fp8_last_error",
+            "vdn_fp8_abi_version"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -72,6 +73,13 @@ FAKE = 1 << 20        # never dereferenced: every call below fails validation fi
     (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 7, None, None, 0, 0, None, 0, FAKE, 4, None), "epilogue"),
     (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 2, None, None, 0, 0, None, 0, FAKE, 4, None), "gate"),
     (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 16, 32, None, 0, None, None, 0, 0, None, 0, FAKE, 4, None), "ldx"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 96, 192, None, 1e-6, None, None, 0, 0, 0, FAKE, 192, None), "head dim"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 128, 256, None, 1e-6, FAKE, FAKE, 72, 72, 0, FAKE, 256, None), "multiple of 16"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 128, 256, None, 1e-6, None, None, 128, 128, 0, FAKE, 256, None), "tables"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 128, 128, None, 1e-6, None, None, 0, 0, 0, FAKE, 256, None), "H * d"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 200, 128, 25600, None, 1e-6, None, None, 0, 0, 0, FAKE, 25600, None), "16384"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE + 8, 4, 2, 128, 256, None, 1e-6, None, None, 0, 0, 0, FAKE, 256, None), "aligned"),
+    (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 128, 256, None, -1.0, None, None, 0, 0, 0, FAKE, 256, None), "eps"),
 ])
 def test_contract_violations_are_einval(call, needle):
     import vdn_fp8._lib as L
@@ -88,6 +96,7 @@ def test_empty_problems_are_no_ops():
     assert lib.vdn_fp8_requantize_weight(None, 0, 8, 8, None, None, 0, 1.0, None, 8, None, None, None) == L.OK
     assert lib.vdn_fp8_norm_quantize_rows(None, 0, 8, 8, None, 1e-6, None, None, 0, None, 0, None, 8, None,
                                           None, 8, None) == L.OK
+    assert lib.vdn_fp8_qk_prep(None, 0, 2, 128, 256, None, 1e-6, None, None, 0, 0, 0, None, 256, None) == L.OK
 
 
 def test_check_raises_reference_exception_types():

@@ -317,3 +317,64 @@ def test_norm_quantize_is_quantize_of_normed():
     q, s, n = O.norm_quantize_rows(x)
     q2, s2 = O.quantize_rows(n)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def _rms_norm_torch64(x_bits, w_bits, eps):
+    import torch.nn.functional as F
+    xt = torch.from_numpy(O.bf16_decode(x_bits).astype(np.float64))
+    wt = None if w_bits is None else torch.from_numpy(O.bf16_decode(w_bits).astype(np.float64))
+    return F.rms_norm(xt, (xt.shape[-1],), wt, float(np.float32(eps))).numpy()
+
+
+def _bits64(v):
+    return O.bf16_encode(np.asarray(v, np.float64).astype(np.float32))
+
+
+def test_qk_prep_identity_rotation_is_rms_norm():
+    """cos = 1, sin = 0: the pass is torch's F.rms_norm (float64), rounded once."""
+    rng = np.random.default_rng(31)
+    T, H, d = 7, 3, 128
+    x = O.bf16_encode(rng.standard_normal((T, H, d), dtype=np.float32) * 3)
+    w = O.bf16_encode(1 + 0.1 * rng.standard_normal(d, dtype=np.float32))
+    ones, zeros = np.ones((T, d), np.float32), np.zeros((T, d), np.float32)
+    got = O.qk_prep(x, w, 1e-6, ones, zeros)
+    want = _bits64(_rms_norm_torch64(x, w, 1e-6))
+    assert np.mean(got == want) > 0.999
+    assert np.array_equal(O.qk_prep(x, w, 1e-6), got)          # no tables: no rotation
+
+
+def test_qk_prep_quarter_turn_and_pass_through():
+    """cos = 0, sin = 1 on the first R channels: out[i] = -n[i + R/2], out[i + R/2] = n[i];
+    channels past R are the plain RMSNorm."""
+    rng = np.random.default_rng(32)
+    T, H, d, R = 5, 4, 128, 64
+    x = O.bf16_encode(rng.standard_normal((T, H, d), dtype=np.float32))
+    n = _rms_norm_torch64(x, None, 1e-6)
+    got = O.bf16_decode(O.qk_prep(x, None, 1e-6, np.zeros((T, R), np.float32), np.ones((T, R), np.float32)))
+    h = R // 2
+    want = n.copy()
+    want[..., :h] = -n[..., h:R]
+    want[..., h:R] = n[..., :h]
+    assert np.mean(got == O.bf16_decode(_bits64(want))) > 0.999
+
+
+def test_qk_prep_is_complex_rotation():
+    """With the usual table layout (cos[i] = cos[i + R/2]), each pair (n[i], n[i + R/2])
+    is multiplied by the complex number c + i s: an independent formulation."""
+    rng = np.random.default_rng(33)
+    T, H, d = 6, 5, 128
+    x = O.bf16_encode(rng.standard_normal((T, H, d), dtype=np.float32) * 0.5)
+    w = O.bf16_encode(1 + 0.05 * rng.standard_normal(d, dtype=np.float32))
+    theta = rng.uniform(-np.pi, np.pi, (T, d // 2))
+    cos = np.concatenate([np.cos(theta), np.cos(theta)], 1).astype(np.float32)
+    sin = np.concatenate([np.sin(theta), np.sin(theta)], 1).astype(np.float32)
+    got = O.bf16_decode(O.qk_prep(x, w, 1e-6, cos, sin)).astype(np.float64)
+    n = _rms_norm_torch64(x, w, 1e-6)
+    c = O.bf16_decode(O.bf16_encode(cos[:, : d // 2])).astype(np.float64)[:, None, :]
+    s = O.bf16_decode(O.bf16_encode(sin[:, : d // 2])).astype(np.float64)[:, None, :]
+    z = (n[..., : d // 2] + 1j * n[..., d // 2:]) * (c + 1j * s)
+    want = np.concatenate([z.real, z.imag], -1)
+    want_b = O.bf16_decode(_bits64(want)).astype(np.float64)
+    assert np.mean(got == want_b) > 0.995
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(got - want) <= ulp)

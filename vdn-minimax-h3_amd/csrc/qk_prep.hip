@@ -1,0 +1,200 @@
+// QK preparation: per-head RMSNorm followed by rotary embedding, one pass.
+//
+// For each token t and head h of q (or k) [T, H, d] (bf16):
+//   rstd    = 1 / sqrt(sum_i x[i]^2 / d + eps)                        (binary32)
+//   n[i]    = (x[i] * rstd) * w[i]                                    (w = 1 if absent)
+//   c[i], s[i] = bf16(cos[t][i]), bf16(sin[t][i])                     (i < rotary_dim)
+//   r[i]    = -n[i + R/2] if i < R/2, n[i - R/2] if R/2 <= i < R      (R = rotary_dim)
+//   out[i]  = bf16(n[i] * c[i] + r[i] * s[i])   for i < R
+//   out[i]  = bf16(n[i])                        for i >= R
+// The chain stays in binary32 and rounds once at the store, as the compiled
+// `_qk_prep` of the reference does (softmax_attention/kernels.py:8-45); the
+// cos/sin tables are rounded to bf16 first, as its `cos.to(x.dtype)` does.
+//
+// Layout: one wave per token, 16-byte chunks (8 elements) with lane L taking
+// chunks L, L + 64, ... A head of d elements is d / 8 consecutive chunks, so
+// with d in {64, 128, 256} every head sits in one group of d / 8 lanes of one
+// sweep: the sum of squares is a butterfly inside the group, and the rotary
+// partner of a chunk (R/2 elements away) is R/16 lanes away in the same group.
+// Each lane's position inside its head is fixed (64 is a multiple of d / 8),
+// so its weight and cos/sin values are loaded once per token.
+#include <stdint.h>
+
+#include "vdn_common.h"
+
+namespace vdn {
+namespace {
+
+constexpr int kLanes = 64;
+constexpr int kWavesPerBlock = 4;   // tokens per workgroup
+
+struct QkArgs {
+    const uint16_t* x;
+    int64_t T, H, d, ldx;
+    const uint16_t* weight;   // [d] or NULL
+    float eps;
+    const void* cos;          // [T, R] (row stride ldcs), binary32 or bf16; NULL when R == 0
+    const void* sin;
+    int64_t R, ldcs;
+    int cs_bf16;
+    uint16_t* out;
+    int64_t ldo;
+};
+
+// Eight table values for elements i0 .. i0 + 7 of row t, rounded to bf16 and
+// returned as binary32.
+__device__ __forceinline__ void load_table8(const QkArgs& p, const void* tab, int64_t t, int i0, float v[8])
+{
+    if (p.cs_bf16) {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(tab) + t * p.ldcs + i0);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(w[e]); v[2 * e + 1] = bf16_hi(w[e]); }
+    } else {
+        const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(tab) + t * p.ldcs + i0);
+        const float4 a = f[0], b = f[1];
+        const float raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t r = pack_bf16x2(raw[e], raw[e + 1]);
+            v[e] = bf16_lo(r);
+            v[e + 1] = bf16_hi(r);
+        }
+    }
+}
+
+// G = d / 8 lanes per head; CPL = chunks per lane.
+template <int G, int CPL>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
+{
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (t >= p.T) return;
+    const int nch = (int)(p.H * G);                  // chunks per token
+    const int j = lane % G;                           // chunk index inside the head
+    const int i0 = 8 * j;                             // first element of this lane's chunks
+
+    // The token's chunks (buffer loads: chunks past the token read zero, no branch).
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.x + t * p.ldx), 0, nch * 16, 0x00020000);
+    uint4 v[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((lane + kLanes * c) * 16), 0, 0));
+
+    float w[8];
+    if (p.weight) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p.weight + i0);
+        const uint32_t ww[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { w[2 * e] = bf16_lo(ww[e]); w[2 * e + 1] = bf16_hi(ww[e]); }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = 1.0f;
+    }
+    const int half = (int)(p.R / 2);
+    const bool rot = i0 < p.R;                        // R % 16 == 0: whole chunks rotate or pass
+    const bool first = i0 < half;                     // partner R/2 elements ahead (sign -1)
+    const int partner = lane + (first ? half / 8 : -(half / 8));
+    float cs[8], sn[8];
+    if (rot) {
+        load_table8(p, p.cos, t, i0, cs);
+        load_table8(p, p.sin, t, i0, sn);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { cs[e] = 1.0f; sn[e] = 0.0f; }
+    }
+
+    uint16_t* orow = p.out + t * p.ldo;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int q = lane + kLanes * c;
+        const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[2 * e] = bf16_lo(xw[e]); x[2 * e + 1] = bf16_hi(xw[e]); }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+        for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, kLanes);
+        const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.d + p.eps);
+        float n[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) n[e] = (x[e] * rstd) * w[e];
+        // every lane takes part in the exchange (the lanes of pass-through chunks
+        // read a value they do not use)
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float pe = __shfl(n[e], rot ? partner : lane, kLanes);
+            const float r = first ? -pe : pe;
+            o[e] = rot ? n[e] * cs[e] + r * sn[e] : n[e];
+        }
+        if (q < nch) {
+            *reinterpret_cast<uint4*>(orow + 8 * q) =
+                make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                           pack_bf16x2(o[6], o[7]));
+        }
+    }
+}
+
+int pick_cpl_qk(int64_t nch)
+{
+    static const int options[] = {1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 28, 32};
+    for (int c : options)
+        if ((int64_t)c * kLanes >= nch) return c;
+    return 0;
+}
+
+template <int G>
+int launch_g(const QkArgs& p, int cpl, hipStream_t stream)
+{
+    const dim3 grid((unsigned)((p.T + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    switch (cpl) {
+#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_qk_prep<G, n>), grid, block, 0, stream, p); break;
+        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
+        VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
+#undef VDN_CASE
+        default: return set_error(VDN_FP8_EINVAL, "qk_prep: unsupported H * d");
+    }
+    return check_launch("qk_prep");
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
+
+}  // namespace
+}  // namespace vdn
+
+using namespace vdn;
+
+extern "C" int vdn_fp8_qk_prep(const void* x, int64_t T, int64_t H, int64_t d, int64_t ldx, const void* weight,
+                               float eps, const void* cos, const void* sin, int64_t rotary_dim, int64_t ldcs,
+                               int cs_bf16, void* out, int64_t ldo, hipStream_t stream)
+{
+    if (T < 0 || H < 0 || d < 0) return set_error(VDN_FP8_EINVAL, "qk_prep: negative shape");
+    if (T == 0 || H == 0) return VDN_FP8_OK;
+    if (!x || !out) return set_error(VDN_FP8_EINVAL, "qk_prep: null pointer");
+    if (d != 64 && d != 128 && d != 256) return set_error(VDN_FP8_EINVAL, "qk_prep: head dim %lld not in {64, 128, 256}", (long long)d);
+    if (rotary_dim < 0 || rotary_dim > d || rotary_dim % 16)
+        return set_error(VDN_FP8_EINVAL, "qk_prep: rotary_dim %lld must be a multiple of 16 in [0, d]", (long long)rotary_dim);
+    if (rotary_dim > 0 && (!cos || !sin || ldcs < rotary_dim))
+        return set_error(VDN_FP8_EINVAL, "qk_prep: rotary tables missing or row stride below rotary_dim");
+    if (ldx % 8 || ldo % 8 || ldx < H * d || ldo < H * d)
+        return set_error(VDN_FP8_EINVAL, "qk_prep: need ldx, ldo multiples of 8 and >= H * d");
+    if (!(eps >= 0.0f)) return set_error(VDN_FP8_EINVAL, "qk_prep: eps must be >= 0");
+    const int64_t csal = cs_bf16 ? 8 : 4;
+    if (!aligned16(x) || !aligned16(out) || (weight && !aligned16(weight)) ||
+        (rotary_dim > 0 && (!aligned16(cos) || !aligned16(sin) || ldcs % csal)))
+        return set_error(VDN_FP8_EINVAL, "qk_prep: misaligned pointer (x, out, weight, cos, sin 16 B; table rows 16 B)");
+    const int64_t nch = H * d / 8;
+    const int cpl = pick_cpl_qk(nch);
+    if (cpl == 0) return set_error(VDN_FP8_EINVAL, "qk_prep: H * d = %lld above the supported 16384", (long long)(H * d));
+    QkArgs p{(const uint16_t*)x, T, H, d, ldx, (const uint16_t*)weight, eps, cos, sin, rotary_dim, ldcs, cs_bf16,
+             (uint16_t*)out, ldo};
+    switch (d) {
+        case 64: return launch_g<8>(p, cpl, stream);
+        case 128: return launch_g<16>(p, cpl, stream);
+        default: return launch_g<32>(p, cpl, stream);
+    }
+}
