@@ -77,6 +77,8 @@ int vdn_fp8_swiglu_quantize_rows(const void *h, int64_t M, int64_t K, int64_t ld
  * modulation (mod_scale, mod_shift: bf16 [mod_rows, K], row stride ldmod) may
  * be NULL (plain RMSNorm). normed, if not NULL, receives n (bf16 [M, K], row
  * stride ldn). x bf16 [M, K] (row stride ldx); y e4m3 [M, K]; y_scale fp32 [M].
+ * y and y_scale may both be NULL when normed is not: the call is then the
+ * pre-norm alone (the compiled `pre`, for a consumer that is not an fp8 linear).
  * Replaces: _pre_ref / the compiled `pre` followed by quantize_rows,
  *           src/models/ops/fused_block.py:41-44,101-108 and
  *           src/models/ops/fp8_linear.py:110-117.
@@ -168,6 +170,24 @@ int vdn_fp8_qk_prep(const void *x, int64_t T, int64_t H, int64_t d, int64_t ldx,
                     const void *weight, float eps, const void *cos, const void *sin,
                     int64_t rotary_dim, int64_t ldcs, int cs_bf16, void *out, int64_t ldo,
                     hipStream_t stream);
+
+/*
+ * The block's gated residual add:
+ *   out[m][n] = bf16(residual[m][n] + gate[i][n] * branch[m][n])    (binary32 inside)
+ * with i = gate_index[m] clamped into [0, gate_rows) (row 0 when gate_index is
+ * NULL). residual, branch, out bf16 [M, N] (row strides ldr, ldb, ldo; out may
+ * alias residual); gate bf16 [gate_rows, N] (row stride ldgate). The same
+ * arithmetic as the GEMM's gate epilogue, for a branch that does not end in
+ * one of this library's GEMMs.
+ * Replaces: _post_ref / the compiled `post`, src/models/ops/fused_block.py:47-49,
+ *           as fast_block_forward applies it (fused_block.py:101-110).
+ * Requires: N and the row strides multiples of 8; residual, gate, branch, out
+ *           16-byte aligned; gate_index 4-byte aligned.
+ */
+int vdn_fp8_gated_residual(const void *residual, int64_t ldr, const void *gate, int64_t ldgate,
+                           const int32_t *gate_index, int64_t gate_rows, const void *branch,
+                           int64_t ldb, void *out, int64_t ldo, int64_t M, int64_t N,
+                           hipStream_t stream);
 
 /* The message of the last failed call on this host thread ("" if none). */
 const char *vdn_fp8_last_error(void);

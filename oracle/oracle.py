@@ -20,7 +20,8 @@ Reference functions restated (paths relative to the reference checkout):
   gelu_tanh             no reference function (the reference FFN is SwiGLU); the textbook
                         tanh approximation of GELU, pinned against torch's
                         F.gelu(approximate="tanh")
-  gated                 src/models/ops/fused_block.py:47-49 (_post_ref)
+  gated / gated_residual  src/models/ops/fused_block.py:47-49 (_post_ref, as the compiled
+                        `post` evaluates it: one bf16 rounding)
   norm_quantize_rows    src/models/ops/fused_block.py:41-44 (_pre_ref, as the compiled
                         `pre` evaluates it: binary32-or-better chain, one bf16 rounding),
                         then quantize_rows on the bf16 result
@@ -245,6 +246,17 @@ def norm_rows(x, weight=None, eps=1e-6, scale=None, shift=None, indices=None, re
         terms = np.abs(v)
     out = bf16_encode(v.astype(np.float32))
     return (out, terms) if return_terms else out
+
+
+def gated_residual(residual, gate, indices, branch):
+    """residual + gate[i] * branch in float64, rounded once to bf16 (through binary32):
+    the compiled `post` (fused_block.py:47-49). residual, branch bf16 bits [M, N]; gate
+    bf16 bits [T, N] (or [N]); indices [M] (clamped into the table) or None (row 0)."""
+    r = bf16_decode(_u16(residual)).astype(np.float64)
+    b = bf16_decode(_u16(branch)).astype(np.float64)
+    g = bf16_decode(_u16(gate)).astype(np.float64).reshape(-1, r.shape[1])
+    idx = np.zeros(r.shape[0], np.int64) if indices is None else np.clip(np.asarray(indices, np.int64), 0, g.shape[0] - 1)
+    return bf16_encode((r + g[idx] * b).astype(np.float32))
 
 
 def norm_quantize_rows(x, weight=None, eps=1e-6, scale=None, shift=None, indices=None):

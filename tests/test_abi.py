@@ -20,7 +20,8 @@ def declared_symbols():
 def test_header_declares_the_abi():
     names = declared_symbols()
     assert {"vdn_fp8_quantize_rows", "vdn_fp8_swiglu_quantize_rows", "vdn_fp8_requantize_weight",
-            "vdn_fp8_gemm", "vdn_fp8_norm_quantize_rows", "vdn_fp8_qk_prep", "vdn_fp8_last_error",
+            "vdn_fp8_gemm", "vdn_fp8_norm_quantize_rows", "vdn_fp8_qk_prep", "vdn_fp8_gated_residual",
+            "vdn_fp8_last_error",
             "vdn_fp8_abi_version"} <= set(names)
 
 
@@ -80,6 +81,14 @@ FAKE = 1 << 20        # never dereferenced: every call below fails validation fi
     (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 200, 128, 25600, None, 1e-6, None, None, 0, 0, 0, FAKE, 25600, None), "16384"),
     (lambda l: l.vdn_fp8_qk_prep(FAKE + 8, 4, 2, 128, 256, None, 1e-6, None, None, 0, 0, 0, FAKE, 256, None), "aligned"),
     (lambda l: l.vdn_fp8_qk_prep(FAKE, 4, 2, 128, 256, None, -1.0, None, None, 0, 0, 0, FAKE, 256, None), "eps"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 8, 8, None, 1e-6, None, None, 0, None, 0, None, 8, None,
+                                            None, 8, None), "only when normed"),
+    (lambda l: l.vdn_fp8_norm_quantize_rows(FAKE, 4, 8, 8, None, 1e-6, None, None, 0, None, 0, FAKE, 8, None,
+                                            FAKE, 8, None), "together"),
+    (lambda l: l.vdn_fp8_gated_residual(FAKE, 8, FAKE, 8, None, 1, FAKE, 8, FAKE, 8, 4, 12, None), "multiples of 8"),
+    (lambda l: l.vdn_fp8_gated_residual(FAKE, 8, FAKE, 8, None, 0, FAKE, 8, FAKE, 8, 4, 8, None), ">= 1 row"),
+    (lambda l: l.vdn_fp8_gated_residual(FAKE, 8, None, 8, None, 1, FAKE, 8, FAKE, 8, 4, 8, None), "null"),
+    (lambda l: l.vdn_fp8_gated_residual(FAKE + 8, 8, FAKE, 8, None, 1, FAKE, 8, FAKE, 8, 4, 8, None), "aligned"),
 ])
 def test_contract_violations_are_einval(call, needle):
     import vdn_fp8._lib as L
@@ -97,6 +106,7 @@ def test_empty_problems_are_no_ops():
     assert lib.vdn_fp8_norm_quantize_rows(None, 0, 8, 8, None, 1e-6, None, None, 0, None, 0, None, 8, None,
                                           None, 8, None) == L.OK
     assert lib.vdn_fp8_qk_prep(None, 0, 2, 128, 256, None, 1e-6, None, None, 0, 0, 0, None, 256, None) == L.OK
+    assert lib.vdn_fp8_gated_residual(None, 8, None, 8, None, 1, None, 8, None, 8, 0, 8, None) == L.OK
 
 
 def test_check_raises_reference_exception_types():

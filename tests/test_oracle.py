@@ -378,3 +378,22 @@ def test_qk_prep_is_complex_rotation():
     assert np.mean(got == want_b) > 0.995
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
     assert np.all(np.abs(got - want) <= ulp)
+
+
+def test_gated_residual_matches_torch_binary32():
+    """The compiled `post` evaluates residual + gate * branch in binary32 (the product of
+    two bf16 values is exact there) and rounds to bf16 once: torch's own binary32
+    arithmetic and casts give the same bits as the oracle's float64 restatement."""
+    rng = np.random.default_rng(51)
+    M, N, T = 64, 96, 3
+    r = O.bf16_encode(rng.standard_normal((M, N), dtype=np.float32))
+    b = O.bf16_encode(rng.standard_normal((M, N), dtype=np.float32) * 5)
+    g = O.bf16_encode(rng.uniform(0, 2, (T, N)).astype(np.float32))
+    idx = rng.integers(0, T, M)
+    t = lambda a: torch.from_numpy(O.bf16_decode(a).astype(np.float32))
+    want = (t(r) + t(g)[torch.from_numpy(idx)] * t(b)).to(torch.bfloat16)
+    want = want.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.gated_residual(r, g, idx, b), want)
+    # the product is exact in binary32: no rounding before the sum
+    prod = O.bf16_decode(g).astype(np.float64)[idx] * O.bf16_decode(b).astype(np.float64)
+    assert np.array_equal(prod, prod.astype(np.float32).astype(np.float64))

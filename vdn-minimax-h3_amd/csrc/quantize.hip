@@ -298,12 +298,20 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
         m2 = absmax_bf16x2(m2, v[c].z);
         m2 = absmax_bf16x2(m2, v[c].w);
     }
+    uint4* nr = reinterpret_cast<uint4*>(p.normed + row * p.ldn);
+    if (!p.y) {                                      // the pre-norm alone (bf16 out)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + kLanes * c;
+            if (idx < nch) nr[idx] = v[c];
+        }
+        return;
+    }
     const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
     const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
     if (lane == 0) p.y_scale[row] = scale;
     const float r = 1.0f / scale;
     uint2* yr = reinterpret_cast<uint2*>(p.y + row * p.ldy);
-    uint4* nr = reinterpret_cast<uint4*>(p.normed + row * p.ldn);
     const bool finite = __builtin_isfinite(scale);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -473,14 +481,16 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: negative shape");
     if (M == 0) return VDN_FP8_OK;
     if (K == 0) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: K must be positive");
-    if (!x || !y || !y_scale) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: null pointer");
+    if (!x || (!y != !y_scale) || (!y && !normed))
+        return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: null pointer (y and y_scale may be NULL together "
+                                         "only when normed is given)");
     if (!mod_scale != !mod_shift) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: scale and shift go together");
-    if (K % 8 || ldx % 8 || ldy % 8 || ldx < K || ldy < K || (normed && (ldn % 8 || ldn < K)) ||
+    if (K % 8 || ldx % 8 || ldx < K || (y && (ldy % 8 || ldy < K)) || (normed && (ldn % 8 || ldn < K)) ||
         (mod_scale && (ldmod % 8 || ldmod < K || mod_rows < 1)))
         return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: need K and the row strides multiples of 8 and >= K, "
                                          "and a modulation table of >= 1 row");
     if (!(eps >= 0.0f)) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: eps must be >= 0");
-    if (!aligned(x, 16) || !aligned(y, 8) || (weight && !aligned(weight, 16)) || (mod_scale && !aligned(mod_scale, 16)) ||
+    if (!aligned(x, 16) || (y && !aligned(y, 8)) || (weight && !aligned(weight, 16)) || (mod_scale && !aligned(mod_scale, 16)) ||
         (mod_shift && !aligned(mod_shift, 16)) || (normed && !aligned(normed, 16)) || (mod_index && !aligned(mod_index, 4)))
         return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: misaligned pointer (x, weight, scale, shift, normed 16 B; y 8 B)");
     const int64_t nch = K / 8;

@@ -11,7 +11,7 @@ from .fp8_linear import (FP8_DTYPE, MIN_WIDTH, SKIP_END_BLOCKS, _FP8_MAX, Fp8Lin
                          convert_linear_to_fp8, per_tensor_gemm, quantize_activation,
                          quantize_rows, quantize_rows_reference, requantize_weight,
                          swiglu_quantize, swiglu_quantize_activation)
-from .fused_block import pre_quantize
+from .fused_block import fast_block_forward, fast_ff_forward, post, pre, pre_quantize
 from .lora import load_external_lora, merge_lora_and_convert, merge_lora_state
 from .softmax_attention import qk_prep
 
@@ -19,5 +19,6 @@ __all__ = [
     "FP8_DTYPE", "MIN_WIDTH", "SKIP_END_BLOCKS", "_FP8_MAX", "Fp8Linear", "convert_linear_to_fp8",
     "per_tensor_gemm", "quantize_activation", "quantize_rows", "quantize_rows_reference",
     "requantize_weight", "swiglu_quantize", "swiglu_quantize_activation", "load_external_lora",
-    "merge_lora_and_convert", "merge_lora_state", "pre_quantize", "qk_prep",
+    "merge_lora_and_convert", "merge_lora_state", "pre_quantize", "qk_prep", "pre", "post",
+    "fast_ff_forward", "fast_block_forward",
 ]

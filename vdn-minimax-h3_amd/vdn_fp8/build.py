@@ -19,7 +19,7 @@ _INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
 LIB_NAME = "libvdnfp8.so"
 LIB_PATH = os.path.join(_PKG, LIB_NAME)
 
-SOURCES = ["capi.hip", "quantize.hip", "lora_requant.hip", "gemm.hip", "qk_prep.hip"]
+SOURCES = ["capi.hip", "quantize.hip", "lora_requant.hip", "gemm.hip", "qk_prep.hip", "block_ops.hip"]
 
 # -ffp-contract=off: the quantizers' binary32 arithmetic is bit-exact only as
 # written (explicit fma where one is meant). Packed fp32 instructions are kept
