@@ -277,6 +277,36 @@ def main():
                                            "under_load": _under_load(lambda: lin_u.forward_quantized(qu, sx0))}
         extra["gemm_qkv_under_load"] = _under_load(lambda: lin.forward_quantized(qx0, sx0))
         del lin_u, qu
+        # the H3 model's widths at one rank's share of a sequence (13107 tokens): fused QKV
+        # [21504 x 5376] + bias, FF projection [28672 x 5376] + bias, FF down [5376 x 14336]
+        # with the block's gate table and residual
+        gh = torch.Generator().manual_seed(13)
+        Mh = 13107
+        xh = torch.randn(Mh, 5376, generator=gh).to(torch.bfloat16).to(dev)
+        qxh, sxh = vdn_fp8.quantize_rows(xh)
+        for name, n_, k_ in (("gemm_h3_qkv", 21504, 5376), ("gemm_h3_ff_proj", 28672, 5376)):
+            wh = (0.02 * torch.randn(n_, k_, generator=gh)).to(torch.bfloat16)
+            bh = (0.01 * torch.randn(n_, generator=gh)).to(torch.bfloat16)
+            lh = _make_linear(wh, bh, dev)
+            ms = _time_region(lambda: lh.forward_quantized(qxh, sxh), reps)
+            tf = wl.linear_flops(Mh, n_, k_) / (ms * 1e-3) / 1e12
+            extra[name] = {"shape": [Mh, n_, k_], "ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                           "frac": round(tf / PEAK_FP8_TFLOPS, 4)}
+            del lh
+        hh3 = torch.randn(Mh, 14336, generator=gh).to(torch.bfloat16).to(dev)
+        qh3, sh3 = vdn_fp8.quantize_rows(hh3)
+        ld = _make_linear((0.02 * torch.randn(5376, 14336, generator=gh)).to(torch.bfloat16), None, dev)
+        gt = (2 * torch.rand(4, 5376, generator=gh)).to(torch.bfloat16).to(dev)
+        gix = torch.randint(0, 4, (Mh,), generator=gh).to(torch.int32).to(dev)
+        ms = _time_region(lambda: ld.forward_quantized(qh3, sh3, epilogue="gate", gate=gt, gate_index=gix,
+                                                       residual=xh), reps)
+        tf = wl.linear_flops(Mh, 5376, 14336) / (ms * 1e-3) / 1e12
+        extra["gemm_h3_ff_down_gate_residual"] = {"shape": [Mh, 5376, 14336], "ms": round(ms, 4),
+                                                  "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP8_TFLOPS, 4)}
+        ms = _time_region(lambda: ld.forward_quantized(qh3, sh3), reps)
+        extra["gemm_h3_ff_down"] = {"shape": [Mh, 5376, 14336], "ms": round(ms, 4),
+                                    "TFLOP/s": round(wl.linear_flops(Mh, 5376, 14336) / (ms * 1e-3) / 1e12, 1)}
+        del ld, hh3, qh3, xh, qxh
         ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
         extra["quantize_rows_13824"] = {"ms": round(ms, 4),
                                         "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
@@ -296,6 +326,15 @@ def main():
         ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
         extra["pre_norm_quantize"] = {"ms": round(ms, 4),
                                       "GB/s": round(wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9, 1)}
+        # the block's gated residual add (`post`) over [M, 5120] with a 2-row gate table
+        from vdn_fp8 import fused_block as FB
+        br_ = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        gtab = (2 * torch.rand(2, K, device=dev)).to(torch.bfloat16)
+        gid = torch.randint(0, 2, (M,), device=dev)
+        ms = _time_region(lambda: FB.post(x, gtab, gid, br_), reps)
+        extra["post_gated_residual"] = {"shape": [M, K], "ms": round(ms, 4),
+                                        "GB/s": round(3 * M * K * 2 / (ms * 1e-3) / 1e9, 1)}
+        del br_
         # QK-norm + rope on q of the QKV output (40 heads of 128, a strided view of the fused
         # [M, 3 x 5120] projection output), fp32 cos/sin tables [M, 128]
         qkv_out = lin.forward_quantized(*vdn_fp8.quantize_rows(x))

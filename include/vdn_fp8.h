@@ -129,7 +129,10 @@ int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
  * bias bf16 [N] or NULL. For VDN_FP8_EPI_GATE: gate bf16 [gate_rows, N] (row
  * stride ldgate), gate_index int32 [M] (NULL = row 0 for every m; an index
  * outside [0, gate_rows) is clamped into it), residual bf16 [M, N] (row stride
- * ldres) or NULL. out bf16 [M, N] (row stride ldo).
+ * ldres) or NULL. out bf16 [M, N] (row stride ldo). With a per-row gate or a
+ * residual and 16-byte aligned rows the call runs two kernels on the stream
+ * (the GEMM writing v, then the gated residual add in place on out); the
+ * result is the same.
  * Replaces: Fp8Linear.forward_quantized, src/models/ops/fp8_linear.py:270-277
  *           (torch._scaled_mm rowwise + bias add); the GELU epilogue has no
  *           reference function; the gate epilogue replaces _post_ref /
@@ -176,7 +179,8 @@ int vdn_fp8_qk_prep(const void *x, int64_t T, int64_t H, int64_t d, int64_t ldx,
  *   out[m][n] = bf16(residual[m][n] + gate[i][n] * branch[m][n])    (binary32 inside)
  * with i = gate_index[m] clamped into [0, gate_rows) (row 0 when gate_index is
  * NULL). residual, branch, out bf16 [M, N] (row strides ldr, ldb, ldo; out may
- * alias residual); gate bf16 [gate_rows, N] (row stride ldgate). The same
+ * alias residual or branch); residual may be NULL (out = bf16(gate[i][n] *
+ * branch[m][n])); gate bf16 [gate_rows, N] (row stride ldgate). The same
  * arithmetic as the GEMM's gate epilogue, for a branch that does not end in
  * one of this library's GEMMs.
  * Replaces: _post_ref / the compiled `post`, src/models/ops/fused_block.py:47-49,

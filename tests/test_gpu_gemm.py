@@ -156,6 +156,32 @@ def test_gemm_many_tiles_gate(device):
            epilogue="gate", gate=gate, gate_index=gi, residual=res)
 
 
+def test_gemm_gate_rows_paths(device):
+    """A per-row gate on 16-byte rows runs as the GEMM then the in-place gated residual
+    kernel; misaligned residual rows take the epilogue inside the GEMM. Both against the
+    oracle: per-row gate without residual (signed zeros kept), and with a residual whose
+    rows start 8 bytes off a 16-byte boundary."""
+    rng = np.random.default_rng(14)
+    M, N, K, T = 520, 1032, 384, 3
+    gate = O.bf16_encode(rng.uniform(-2, 2, (T, N)).astype(np.float32))
+    gate[1, :8] = 0x8000                                     # -0 gates: -0 * v keeps its sign
+    gi = rng.integers(0, T, M).astype(np.int32)
+    x, w = _rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.05)
+    _check(x, w, None, device, epilogue="gate", gate=gate, gate_index=gi)
+    f = _linear(w, None, device)
+    qx, sx = vdn_fp8.quantize_rows(from_bits(x, device))
+    resbuf = from_bits(_rand(rng, (M, N + 4), 1.0), device)
+    res = resbuf[:, 4:]                                      # rows 8 bytes off 16-byte alignment
+    out = f.forward_quantized(qx, sx, epilogue="gate", gate=from_bits(gate, device),
+                              gate_index=torch.from_numpy(gi).to(device), residual=res)
+    torch.cuda.synchronize()
+    want = O.dequant_linear(codes(qx), sx.cpu().numpy().ravel(), codes(f.weight_fp8),
+                            f.weight_scale.cpu().numpy().ravel(), epilogue="gate", gate=gate, gate_index=gi,
+                            residual=bits(res))
+    got = O.bf16_decode(bits(out))
+    assert O.rel_l2(got, want) <= 1e-3 and np.mean(got == want) >= 0.98
+
+
 def test_gemm_single_workload(device):
     """1024 x 1024 x 1024 single linear, seed 0 (the reference's CPU-runnable case)."""
     x, w, b = workloads.dit_single()
@@ -184,6 +210,24 @@ def test_gemm_ffn_down_attn_out_workload(device):
     g = bits(gate)
     _check(bits(xd), bits(wd), None, device, rows=_sample_rows(xd.shape[0], seed=2), epilogue="gate", gate=g)
     _check(bits(xo), bits(wo), None, device, rows=_sample_rows(xo.shape[0], seed=3), epilogue="gate", gate=g)
+
+
+def test_gemm_h3_shapes(device):
+    """The H3 model's own widths at one rank's share of a sequence (13107 tokens): fused
+    QKV [21504 x 5376] with bias, and the FF down projection [5376 x 14336] with the
+    block's per-token gate table and residual (fast_block_forward's fused form)."""
+    rng = np.random.default_rng(13)
+    M = 13107
+    print("gemm H3 QKV 13107 x 21504 x 5376", flush=True)
+    _check(_rand(rng, (M, 5376), 1.0), _rand(rng, (21504, 5376), 0.02), _rand(rng, (21504,), 0.01), device,
+           rows=_sample_rows(M, 128, seed=4))
+    print("gemm H3 FF down 13107 x 5376 x 14336, gate table + residual", flush=True)
+    T = 4
+    gate = O.bf16_encode(rng.uniform(0, 2, (T, 5376)).astype(np.float32))
+    gi = rng.integers(0, T, M).astype(np.int32)
+    _check(_rand(rng, (M, 14336), 0.5), _rand(rng, (5376, 14336), 0.02), None, device,
+           rows=_sample_rows(M, 128, seed=5), epilogue="gate", gate=gate, gate_index=gi,
+           residual=_rand(rng, (M, 5376), 1.0))
 
 
 def test_gemm_exact_small_integers(device):

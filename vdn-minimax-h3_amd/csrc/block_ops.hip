@@ -2,14 +2,16 @@
 // reference, src/models/ops/fused_block.py:47-49,101-110):
 //
 //   out[m][n] = bf16(residual[m][n] + gate[i][n] * branch[m][n]),   i = gate_index[m]
+//   out[m][n] = bf16(gate[i][n] * branch[m][n])                       (no residual)
 //
 // in binary32 with one rounding (the product of two bf16 values is exact in
 // binary32, so the only roundings are the sum's and the store's). The same
 // arithmetic as the GEMM's gate epilogue, for a branch whose last op is not one
 // of this library's GEMMs (the attention sub-layer).
 //
-// Layout: one workgroup per 2048-element piece of a row (256 threads x 8
-// elements, 16-byte loads and stores); the grid is rows x pieces.
+// Layout: one wave per row (four rows per workgroup); lane L takes the row's
+// 16-byte chunks L, L + 64, ..., four at a time with all their loads issued
+// before any is used.
 #include <stdint.h>
 
 #include "vdn_common.h"
@@ -17,36 +19,76 @@
 namespace vdn {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kPiece = kThreads * 8;
+constexpr int kLanes = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBatch = 4;            // chunks per lane in flight
 
-__global__ __launch_bounds__(kThreads) void k_gated_residual(
-    const uint16_t* __restrict__ residual, int64_t ldr, const uint16_t* __restrict__ gate, int64_t ldgate,
-    const int32_t* __restrict__ gate_index, int64_t gate_rows, const uint16_t* __restrict__ branch, int64_t ldb,
-    uint16_t* out, int64_t ldo, int64_t N)
+template <bool RES>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
+    const uint16_t* residual, int64_t ldr, const uint16_t* __restrict__ gate, int64_t ldgate,
+    const int32_t* __restrict__ gate_index, int64_t gate_rows, const uint16_t* branch, int64_t ldb,
+    uint16_t* out, int64_t ldo, int64_t M, int64_t N)   // out may alias residual or branch
 {
-    const int64_t m = blockIdx.x;
-    const int64_t n = (int64_t)blockIdx.y * kPiece + 8 * threadIdx.x;
-    if (n >= N) return;
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t m = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (m >= M) return;
     int64_t gi = 0;
     if (gate_index) gi = min(max((int64_t)gate_index[m], (int64_t)0), gate_rows - 1);
-    const uint4 r = *reinterpret_cast<const uint4*>(residual + m * ldr + n);
-    const uint4 g = *reinterpret_cast<const uint4*>(gate + gi * ldgate + n);
-    const uint4 b = *reinterpret_cast<const uint4*>(branch + m * ldb + n);
-    const uint32_t rw[4] = {r.x, r.y, r.z, r.w}, gw[4] = {g.x, g.y, g.z, g.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    uint32_t o[4];
+    const int nch = (int)(N >> 3);
+    const uint4* rr = reinterpret_cast<const uint4*>(residual + m * ldr);
+    const uint4* gr = reinterpret_cast<const uint4*>(gate + gi * ldgate);
+    const uint4* br = reinterpret_cast<const uint4*>(branch + m * ldb);
+    uint4* orow = reinterpret_cast<uint4*>(out + m * ldo);
+    for (int c0 = lane; c0 < nch; c0 += kBatch * kLanes) {
+        uint4 r[kBatch], g[kBatch], b[kBatch];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float lo = bf16_lo(rw[e]) + bf16_lo(gw[e]) * bf16_lo(bw[e]);
-        const float hi = bf16_hi(rw[e]) + bf16_hi(gw[e]) * bf16_hi(bw[e]);
-        o[e] = pack_bf16x2(lo, hi);
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j * kLanes;
+            const bool ok = c < nch;
+            r[j] = (RES && ok) ? rr[c] : make_uint4(0u, 0u, 0u, 0u);
+            g[j] = ok ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
+            b[j] = ok ? br[c] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j * kLanes;
+            if (c >= nch) continue;
+            const uint32_t rw[4] = {r[j].x, r[j].y, r[j].z, r[j].w}, gw[4] = {g[j].x, g[j].y, g[j].z, g[j].w},
+                           bw[4] = {b[j].x, b[j].y, b[j].z, b[j].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // without a residual the product is stored as it is (no + 0: that would turn -0 into +0)
+                float lo = bf16_lo(gw[e]) * bf16_lo(bw[e]);
+                float hi = bf16_hi(gw[e]) * bf16_hi(bw[e]);
+                if (RES) { lo = bf16_lo(rw[e]) + lo; hi = bf16_hi(rw[e]) + hi; }
+                o[e] = pack_bf16x2(lo, hi);
+            }
+            orow[c] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     }
-    *reinterpret_cast<uint4*>(out + m * ldo + n) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 }  // namespace
+
+// Launch without argument checks (the callers have made them): also the second
+// pass of the GEMM's per-row gate / residual epilogue, in place on its output.
+int launch_gated_residual(const uint16_t* residual, int64_t ldr, const uint16_t* gate, int64_t ldgate,
+                          const int32_t* gate_index, int64_t gate_rows, const uint16_t* branch, int64_t ldb,
+                          uint16_t* out, int64_t ldo, int64_t M, int64_t N, hipStream_t stream)
+{
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    if (residual)
+        hipLaunchKernelGGL(k_gated_residual<true>, grid, block, 0, stream, residual, ldr, gate, ldgate, gate_index,
+                           gate_rows, branch, ldb, out, ldo, M, N);
+    else
+        hipLaunchKernelGGL(k_gated_residual<false>, grid, block, 0, stream, residual, ldr, gate, ldgate, gate_index,
+                           gate_rows, branch, ldb, out, ldo, M, N);
+    return check_launch("gated_residual");
+}
+
 }  // namespace vdn
 
 using namespace vdn;
@@ -58,20 +100,16 @@ extern "C" int vdn_fp8_gated_residual(const void* residual, int64_t ldr, const v
 {
     if (M < 0 || N < 0) return set_error(VDN_FP8_EINVAL, "gated_residual: negative shape");
     if (M == 0 || N == 0) return VDN_FP8_OK;
-    if (!residual || !gate || !branch || !out) return set_error(VDN_FP8_EINVAL, "gated_residual: null pointer");
-    if (N % 8 || ldr % 8 || ldgate % 8 || ldb % 8 || ldo % 8 || ldr < N || ldb < N || ldo < N ||
+    if (!gate || !branch || !out) return set_error(VDN_FP8_EINVAL, "gated_residual: null pointer");
+    if (N % 8 || (residual && (ldr % 8 || ldr < N)) || ldgate % 8 || ldb % 8 || ldo % 8 || ldb < N || ldo < N ||
         (gate_rows > 1 && ldgate < N) || gate_rows < 1)
         return set_error(VDN_FP8_EINVAL, "gated_residual: need N and the row strides multiples of 8 and >= N, "
                                          "and a gate table of >= 1 row");
-    if (!aligned16(residual) || !aligned16(gate) || !aligned16(branch) || !aligned16(out) ||
+    if ((residual && !aligned16(residual)) || !aligned16(gate) || !aligned16(branch) || !aligned16(out) ||
         (gate_index && ((uintptr_t)gate_index % 4)))
         return set_error(VDN_FP8_EINVAL, "gated_residual: misaligned pointer (residual, gate, branch, out 16 B)");
-    if (M > 0x7fffffffLL) return set_error(VDN_FP8_EINVAL, "gated_residual: too many rows");
-    const int64_t pieces = (N + kPiece - 1) / kPiece;
-    if (pieces > 65535) return set_error(VDN_FP8_EINVAL, "gated_residual: rows too long");
-    const dim3 grid((unsigned)M, (unsigned)pieces), block(kThreads);
-    hipLaunchKernelGGL(k_gated_residual, grid, block, 0, stream, (const uint16_t*)residual, ldr,
-                       (const uint16_t*)gate, ldgate, gate_index, gate_rows, (const uint16_t*)branch, ldb,
-                       (uint16_t*)out, ldo, N);
-    return check_launch("gated_residual");
+    if (M / kWavesPerBlock >= 0x7fffffffLL || N >= 0x7fffffffLL)
+        return set_error(VDN_FP8_EINVAL, "gated_residual: problem too large");
+    return launch_gated_residual((const uint16_t*)residual, ldr, (const uint16_t*)gate, ldgate, gate_index, gate_rows,
+                                 (const uint16_t*)branch, ldb, (uint16_t*)out, ldo, M, N, stream);
 }

@@ -700,6 +700,10 @@ int device_cus()
 }
 
 }  // namespace
+
+int launch_gated_residual(const uint16_t* residual, int64_t ldr, const uint16_t* gate, int64_t ldgate,
+                          const int32_t* gate_index, int64_t gate_rows, const uint16_t* branch, int64_t ldb,
+                          uint16_t* out, int64_t ldo, int64_t M, int64_t N, hipStream_t stream);
 }  // namespace vdn
 
 using namespace vdn;
@@ -747,8 +751,19 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     // per-row gate or residual (a gate table of one row is staged like the bias)
     const bool gate_broadcast = epilogue == VDN_FP8_EPI_GATE && !residual && (gate_rows == 1 || !gate_index) &&
                                 aligned(gate, 16);
-    const bool fast = (epilogue != VDN_FP8_EPI_GATE || gate_broadcast) && N % 8 == 0 && ldo % 8 == 0 &&
-                      aligned(out, 16) && (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
+    const bool out16 = N % 8 == 0 && ldo % 8 == 0 && aligned(out, 16) && (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
+    const bool fast = (epilogue != VDN_FP8_EPI_GATE || gate_broadcast) && out16;
+    // A per-row gate or a residual on 16-byte rows: the fast GEMM writes v, then the
+    // gated residual kernel forms bf16(residual + gate[i] * v) in place -- the same
+    // two roundings as the epilogue, without its per-row loads inside the GEMM.
+    if (main && epilogue == VDN_FP8_EPI_GATE && !gate_broadcast && out16 && aligned(gate, 16) && ldgate % 8 == 0 &&
+        (!residual || (aligned(residual, 16) && ldres % 8 == 0))) {
+        hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true>), grid, block, 0, stream, p);
+        const int st = check_launch("gemm");
+        if (st != VDN_FP8_OK) return st;
+        return launch_gated_residual((const uint16_t*)residual, ldres, (const uint16_t*)gate, ldgate, gate_index,
+                                     gate_rows, (const uint16_t*)out, ldo, (uint16_t*)out, ldo, M, N, stream);
+    }
 #define VDN_LAUNCH(E)                                                                          \
     do {                                                                                       \
         if (main && fast) hipLaunchKernelGGL((k_gemm_fp8<E, true>), grid, block, 0, stream, p);  \
