@@ -92,6 +92,25 @@ def _under_load(fn, seconds=2.0):
             "socket_w": round(sum(pw) / len(pw)) if pw else None, "samples": len(clk)}
 
 
+def _time_pair(fa, fb, reps):
+    """Mean ms of fa() and of fb(), launched alternately (a, b, a, b, ...) so that a clock
+    that drifts while the part heats up weighs on both alike."""
+    import torch
+    fa(), fb()
+    torch.cuda.synchronize()
+    ev = _events(4 * reps)
+    for i in range(reps):
+        ev[4 * i].record()
+        fa()
+        ev[4 * i + 1].record()
+        fb()
+        ev[4 * i + 2].record()
+    torch.cuda.synchronize()
+    ta = sum(ev[4 * i].elapsed_time(ev[4 * i + 1]) for i in range(reps)) / reps
+    tb = sum(ev[4 * i + 1].elapsed_time(ev[4 * i + 2]) for i in range(reps)) / reps
+    return ta, tb
+
+
 def _time_region(fn, reps):
     """Mean ms of fn() over reps launches, from HIP events on the current stream (after one
     untimed call)."""
@@ -306,7 +325,30 @@ def main():
         ms = _time_region(lambda: ld.forward_quantized(qh3, sh3), reps)
         extra["gemm_h3_ff_down"] = {"shape": [Mh, 5376, 14336], "ms": round(ms, 4),
                                     "TFLOP/s": round(wl.linear_flops(Mh, 5376, 14336) / (ms * 1e-3) / 1e12, 1)}
-        del ld, hh3, qh3, xh, qxh
+        # the H3 FF sub-layer of fast_block_forward, per rank: fused (pre-norm + quantize,
+        # projection GEMM, SwiGLU + quantize, down GEMM with the gate table and residual) vs
+        # the same kernels with every stretch written out in bf16 (pre, quantize, GEMM,
+        # swiglu + quantize, GEMM, post)
+        from vdn_fp8 import fused_block as FB
+        lp = _make_linear((0.02 * torch.randn(28672, 5376, generator=gh)).to(torch.bfloat16),
+                          (0.01 * torch.randn(28672, generator=gh)).to(torch.bfloat16), dev)
+        nw = (1 + 0.05 * torch.randn(5376, generator=gh)).to(torch.bfloat16).to(dev)
+        tsc = (0.2 * torch.randn(4, 5376, generator=gh)).to(torch.bfloat16).to(dev)
+        tsh = (0.2 * torch.randn(4, 5376, generator=gh)).to(torch.bfloat16).to(dev)
+
+        def ff_fused():
+            yq, ys = FB.pre_quantize(xh, nw, 1e-6, tsc, tsh, gix)
+            a, s_ = vdn_fp8.swiglu_quantize(lp.forward_quantized(yq, ys))
+            return ld.forward_quantized(a, s_, epilogue="gate", gate=gt, gate_index=gix, residual=xh)
+
+        def ff_unfused():
+            n_ = FB.pre(xh, nw, 1e-6, tsc, tsh, gix)
+            a, s_ = vdn_fp8.swiglu_quantize(lp.forward_quantized(*vdn_fp8.quantize_rows(n_)))
+            return FB.post(xh, gt, gix, ld.forward_quantized(a, s_))
+
+        t_f, t_u = _time_pair(ff_fused, ff_unfused, reps)
+        extra["ff_sublayer_h3"] = {"tokens": Mh, "fused_ms": round(t_f, 4), "unfused_ms": round(t_u, 4)}
+        del ld, lp, hh3, qh3, xh, qxh
         ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
         extra["quantize_rows_13824"] = {"ms": round(ms, 4),
                                         "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}

@@ -87,6 +87,10 @@ class _FF(nn.Module):
         super().__init__()
         self.net = nn.ModuleList([_SwiGLU(proj), nn.Dropout(0.0), down])
 
+    def forward(self, x):                       # diffusers' FeedForward: the net in order
+        swiglu, drop, down = self.net
+        return down(drop(FB._swiglu_ref(swiglu.proj(x))))
+
 
 class _AdaLN(nn.Module):
     def __init__(self, table):
@@ -186,3 +190,23 @@ def test_fast_ff_forward_matches_oracle_chain(device):
     print(f"fast_ff_forward vs oracle chain: rel_l2 {err:.2e}, identical {np.mean(got == want):.3f}", flush=True)
     assert err <= 1e-2
     assert np.mean(got == want) >= 0.75
+
+
+def test_fast_block_forward_bf16_ff(device):
+    """A block whose feed-forward stays bf16 (no Fp8Linear): pre, the module, post."""
+    M, C, I, T = 48, 512, 256, 2
+    blk = _Block(C, I, T, device, seed=3)
+    g = torch.Generator().manual_seed(9)
+    proj = nn.Linear(C, 2 * I, dtype=torch.bfloat16).to(device)
+    down = nn.Linear(I, C, dtype=torch.bfloat16).to(device)
+    blk.ff = _FF(proj, down)
+    hidden = torch.randn(M, C, generator=g).to(torch.bfloat16).to(device)
+    idx = torch.randint(0, T, (M,), generator=g).to(device)
+    with torch.no_grad():
+        got = FB.fast_block_forward(blk, hidden, None, idx, None)
+        s1, c1, g1, s2, c2, g2 = blk.adaln_proj(None)
+        h = FB.post(hidden, g1, idx, blk.attn(FB.pre(hidden, blk.norm1.weight, blk.norm1.eps, c1, s1, idx)))
+        n2 = FB.pre(h, blk.norm2.weight, blk.norm2.eps, c2, s2, idx)
+        want = FB.post(h, g2, idx, down(FB._swiglu_ref(proj(n2))))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

@@ -69,8 +69,6 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
     }
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
-
 }  // namespace
 
 // Launch without argument checks (the callers have made them): also the second
@@ -105,7 +103,7 @@ extern "C" int vdn_fp8_gated_residual(const void* residual, int64_t ldr, const v
         (gate_rows > 1 && ldgate < N) || gate_rows < 1)
         return set_error(VDN_FP8_EINVAL, "gated_residual: need N and the row strides multiples of 8 and >= N, "
                                          "and a gate table of >= 1 row");
-    if ((residual && !aligned16(residual)) || !aligned16(gate) || !aligned16(branch) || !aligned16(out) ||
+    if ((residual && !aligned(residual, 16)) || !aligned(gate, 16) || !aligned(branch, 16) || !aligned(out, 16) ||
         (gate_index && ((uintptr_t)gate_index % 4)))
         return set_error(VDN_FP8_EINVAL, "gated_residual: misaligned pointer (residual, gate, branch, out 16 B)");
     if (M / kWavesPerBlock >= 0x7fffffffLL || N >= 0x7fffffffLL)

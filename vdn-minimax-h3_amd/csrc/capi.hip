@@ -25,6 +25,26 @@ int check_launch(const char* what)
     return VDN_FP8_OK;
 }
 
+int device_cus()
+{
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cached[dev] > 0) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cached[dev] = n;
+    return n;
+}
+
+int pick_cpl(int64_t nch)
+{
+    static const int options[] = {1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 28, 32};
+    for (int c : options)
+        if ((int64_t)c * 64 >= nch) return c;
+    return 0;
+}
+
 }  // namespace vdn
 
 extern "C" const char* vdn_fp8_last_error(void) { return vdn::g_last_error; }

@@ -677,8 +677,6 @@ void k_gemm_fp8_ktail(GemmArgs p)
     }
 }
 
-bool aligned(const void* q, uintptr_t a) { return ((uintptr_t)q % a) == 0; }
-
 // K-block rotation of the main kernel: tiles with (tm + tn) odd start one block
 // later, so the workgroups sharing an X or W panel do not all miss the same
 // lines at once (and strided rows do not hit the same memory channels in
@@ -687,17 +685,6 @@ constexpr int kPhaseMod = 2, kPhaseStep = 1;
 
 // Compute units of the current device (the persistent kernel's grid), cached per
 // device; 0 if the runtime cannot say.
-int device_cus()
-{
-    static int cached[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < 64) cached[dev] = n;
-    return n;
-}
 
 }  // namespace
 

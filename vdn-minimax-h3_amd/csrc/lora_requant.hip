@@ -384,18 +384,6 @@ void launch_rp(const Args& p, bool merge_only, int cus, hipStream_t st)
     hipLaunchKernelGGL((k_lora_stripes<RP, kQuantize, BVEC>), g2, block, 0, st, p);
 }
 
-int device_cus_lora()
-{
-    static int cached[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < 64) cached[dev] = n;
-    return n;
-}
-
 }  // namespace
 
 int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, const uint16_t* a,
@@ -418,7 +406,7 @@ int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, co
     const bool merge_only = wq == nullptr;
     const int b_vec = (rank % 8 == 0) && ((uintptr_t)b % 16 == 0);
     const int wm16 = w_merged && ((uintptr_t)w_merged % 16 == 0);
-    const int cus = device_cus_lora();
+    const int cus = device_cus();
     if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "requantize_weight: cannot query the device's compute units");
     Args p{w, N, K, ldw, a, b, rank, b_vec, lora_scale, wq, ldq, w_scale, w_merged, wm16,
            (int)((K + kTileCols - 1) / kTileCols), (int)((N + kTileRows - 1) / kTileRows)};

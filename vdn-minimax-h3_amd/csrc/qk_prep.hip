@@ -139,14 +139,6 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     }
 }
 
-int pick_cpl_qk(int64_t nch)
-{
-    static const int options[] = {1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 28, 32};
-    for (int c : options)
-        if ((int64_t)c * kLanes >= nch) return c;
-    return 0;
-}
-
 template <int G>
 int launch_g(const QkArgs& p, int cpl, hipStream_t stream)
 {
@@ -160,8 +152,6 @@ int launch_g(const QkArgs& p, int cpl, hipStream_t stream)
     }
     return check_launch("qk_prep");
 }
-
-bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 }  // namespace
 }  // namespace vdn
@@ -184,11 +174,11 @@ extern "C" int vdn_fp8_qk_prep(const void* x, int64_t T, int64_t H, int64_t d, i
         return set_error(VDN_FP8_EINVAL, "qk_prep: need ldx, ldo multiples of 8 and >= H * d");
     if (!(eps >= 0.0f)) return set_error(VDN_FP8_EINVAL, "qk_prep: eps must be >= 0");
     const int64_t csal = cs_bf16 ? 8 : 4;
-    if (!aligned16(x) || !aligned16(out) || (weight && !aligned16(weight)) ||
-        (rotary_dim > 0 && (!aligned16(cos) || !aligned16(sin) || ldcs % csal)))
+    if (!aligned(x, 16) || !aligned(out, 16) || (weight && !aligned(weight, 16)) ||
+        (rotary_dim > 0 && (!aligned(cos, 16) || !aligned(sin, 16) || ldcs % csal)))
         return set_error(VDN_FP8_EINVAL, "qk_prep: misaligned pointer (x, out, weight, cos, sin 16 B; table rows 16 B)");
     const int64_t nch = H * d / 8;
-    const int cpl = pick_cpl_qk(nch);
+    const int cpl = pick_cpl(nch);
     if (cpl == 0) return set_error(VDN_FP8_EINVAL, "qk_prep: H * d = %lld above the supported 16384", (long long)(H * d));
     QkArgs p{(const uint16_t*)x, T, H, d, ldx, (const uint16_t*)weight, eps, cos, sin, rotary_dim, ldcs, cs_bf16,
              (uint16_t*)out, ldo};

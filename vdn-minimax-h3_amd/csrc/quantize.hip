@@ -405,15 +405,6 @@ void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int6
 }
 
 // Smallest instantiated chunks-per-lane that covers nch chunks, 0 for the wide kernel.
-int pick_cpl(int64_t nch)
-{
-    static const int options[] = {1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 28, 32};
-    for (int c : options)
-        if ((int64_t)c * kLanes >= nch) return c;
-    return 0;
-}
-
-bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
 

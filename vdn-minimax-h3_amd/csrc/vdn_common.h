@@ -21,6 +21,15 @@ namespace vdn {
 int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device); 0 if it cannot be queried.
+int device_cus();
+
+// Smallest 16-byte-chunks-per-lane template instance (1..32) that covers a row of
+// nch chunks with one wave; 0 above 32 x 64 chunks.
+int pick_cpl(int64_t nch);
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
 // ---------------------------------------------------------------------------
 // device: bf16 / e4m3 conversions
 // ---------------------------------------------------------------------------
