@@ -63,6 +63,29 @@ __device__ __forceinline__ void load_table8(const QkArgs& p, const void* tab, in
     }
 }
 
+// Lane exchanges inside a 16-lane DPP row (d = 128: one head per row), as
+// register moves rather than LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4e;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i within each half row
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i within each row
+constexpr int kDppRor8 = 0x128;        // lane i <- lane (i + 8) mod 16 within each row
+
+// Sum over the 16 lanes of a row, every lane receiving it.
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    v += dpp_f32<kDppMirror>(v);
+    return v;
+}
+
 // G = d / 8 lanes per head; CPL = chunks per lane.
 template <int G, int CPL>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
@@ -96,6 +119,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     const bool rot = i0 < p.R;                        // R % 16 == 0: whole chunks rotate or pass
     const bool first = i0 < half;                     // partner R/2 elements ahead (sign -1)
     const int partner = lane + (first ? half / 8 : -(half / 8));
+    const bool full_rot = p.R == p.d;                 // uniform
     float cs[8], sn[8];
     if (rot) {
         load_table8(p, p.cos, t, i0, cs);
@@ -116,8 +140,12 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+        if (G == 16) {
+            ss = row16_sum(ss);
+        } else {
 #pragma unroll
-        for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, kLanes);
+            for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, kLanes);
+        }
         const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.d + p.eps);
         float n[8];
 #pragma unroll
@@ -125,11 +153,20 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
         // every lane takes part in the exchange (the lanes of pass-through chunks
         // read a value they do not use)
         float o[8];
+        if (G == 16 && full_rot) {
+            // R = d = 128: the partner chunk is 8 lanes away inside the row
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float pe = __shfl(n[e], rot ? partner : lane, kLanes);
-            const float r = first ? -pe : pe;
-            o[e] = rot ? n[e] * cs[e] + r * sn[e] : n[e];
+            for (int e = 0; e < 8; ++e) {
+                const float pe = dpp_f32<kDppRor8>(n[e]);
+                o[e] = n[e] * cs[e] + (first ? -pe : pe) * sn[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float pe = __shfl(n[e], rot ? partner : lane, kLanes);
+                const float r = first ? -pe : pe;
+                o[e] = rot ? n[e] * cs[e] + r * sn[e] : n[e];
+            }
         }
         if (q < nch) {
             *reinterpret_cast<uint4*>(orow + 8 * q) =
