@@ -107,3 +107,38 @@ def test_qk_prep_qkv_workload_rows(device):
     gv, wv = O.bf16_decode(got).astype(np.float64), O.bf16_decode(want).astype(np.float64)
     assert np.all(np.abs(gv - wv) <= _ulp(np.maximum(np.abs(wv), terms)))
     assert np.mean(got == want) >= 0.99
+
+
+def test_qkv_shares_one_quantization(device):
+    """softmax_attention.qkv on fp8 projections: q/k/v equal the three forward_quantized
+    calls on one quantization of x (bit for bit), q/k the qk_prep of the raw projections."""
+    import torch.nn as nn
+    from vdn_fp8 import softmax_attention as SA
+    T, H, d = 300, 8, 128
+    C = H * d
+    g = torch.Generator().manual_seed(5)
+    lins = []
+    for _ in range(3):
+        l = nn.Linear(C, C, dtype=torch.bfloat16)
+        with torch.no_grad():
+            l.weight.copy_((0.02 * torch.randn(C, C, generator=g)).to(torch.bfloat16))
+            l.bias.copy_((0.01 * torch.randn(C, generator=g)).to(torch.bfloat16))
+        lins.append(vdn_fp8.Fp8Linear(l.to(device)))
+    nq, nk = nn.RMSNorm(d, eps=1e-6, dtype=torch.bfloat16).to(device), nn.RMSNorm(d, eps=1e-5, dtype=torch.bfloat16).to(device)
+    with torch.no_grad():
+        nq.weight.copy_((1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16))
+        nk.weight.copy_((1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16))
+    x = torch.randn(T, C, generator=g).to(torch.bfloat16).to(device)
+    th = torch.rand(T, d // 2, generator=g) * 6.28
+    cos = torch.cat([th.cos(), th.cos()], 1).to(device)
+    sin = torch.cat([th.sin(), th.sin()], 1).to(device)
+    with torch.no_grad():
+        q, k, v, (qr, kr, vr) = SA.qkv(x, *lins, H, nq, nk, (cos, sin))
+        xq, xs = vdn_fp8.quantize_rows(x)
+        want = [l.forward_quantized(xq, xs).unflatten(-1, (H, d)) for l in lins]
+        wq = vdn_fp8.qk_prep(want[0], nq.weight, nq.eps, cos, sin)
+        wk = vdn_fp8.qk_prep(want[1], nk.weight, nk.eps, cos, sin)
+    torch.cuda.synchronize()
+    assert q.shape == k.shape == v.shape == (T, H, d)
+    assert torch.equal(qr, want[0]) and torch.equal(kr, want[1]) and torch.equal(v, want[2]) and vr is v
+    assert torch.equal(q, wq) and torch.equal(k, wk)

@@ -58,3 +58,28 @@ def qk_prep(t, weight, eps, cos=None, sin=None):
 
 # The reference's name (softmax_attention/kernels.py:33).
 _qk_prep = qk_prep
+
+
+def qkv(x, to_q, to_k, to_v, heads, norm_q, norm_k, rotary_emb=None):
+    """The inference body of `HybridAttention._qkv` (hybrid_attention.py:108-137) on this
+    library: with fp8 projections x is quantized ONCE and shared by the three GEMMs
+    (hybrid_attention.py:118-124), then QK-norm + rope run as one pass each (`_qk_prep`,
+    :128-130). x [T, hidden] bf16; to_q/k/v the projection modules (Fp8Linear or any
+    callable); norm_q/norm_k modules with `.weight` and `.eps` (RMSNorm); rotary_emb
+    (cos, sin) [T, R] or None. Returns (query, key, value, (query_raw, key_raw, value)),
+    everything [T, heads, d] -- the raw q/k are the ones the linear branch consumes.
+    Without rotary_emb the norms alone run (the same kernel with no rotation), as the
+    reference's eager branch would apply them."""
+    from .fp8_linear import Fp8Linear, quantize_activation
+
+    projections = (to_q, to_k, to_v)
+    if all(isinstance(p, Fp8Linear) for p in projections):
+        x_fp8, x_scale = quantize_activation(x)
+        out = [p.forward_quantized(x_fp8, x_scale, out_dtype=x.dtype) for p in projections]
+    else:
+        out = [p(x) for p in projections]
+    query_raw, key_raw, value = (t.unflatten(-1, (heads, -1)) for t in out)
+    cos, sin = (None, None) if rotary_emb is None else rotary_emb
+    query = qk_prep(query_raw, norm_q.weight, norm_q.eps, cos, sin)
+    key = qk_prep(key_raw, norm_k.weight, norm_k.eps, cos, sin)
+    return query, key, value, (query_raw, key_raw, value)
