@@ -19,7 +19,11 @@
  * path).  Raw binary32 quotients differ only where x is a bf16 subnormal and
  * the remainder underflows; there the quotient is below 2^-26 and encodes to
  * a signed zero either way, which this program confirms.
- * Returns nonzero on any code mismatch and prints a summary.
+ * For the weight path the kernels go further: there x and bf16(s) are both
+ * bf16, and the single product RN(x * r) rounds to the same bf16 value as the
+ * IEEE quotient for every pair (an 8-bit by 8-bit quotient never lies within
+ * the product's error of a bf16 rounding midpoint); this is checked too.
+ * Returns nonzero on any mismatch and prints a summary.
  *
  * Build: gcc -O2 -ffp-contract=off -fopenmp division_check.c ../../oracle/fp8_oracle.c -lm -lpthread
  */
@@ -34,11 +38,11 @@ static uint16_t f2b(float f) { uint32_t u; memcpy(&u, &f, 4); u += 0x7fffu + ((u
 /* fp32 -> e4m3 (RNE, |x| > 464 -> NaN, sign kept): the oracle's encoder. */
 uint8_t oracle_e4m3_from_f32(float f);
 
-static long raw_mismatch_total = 0, raw_mismatch_big = 0;
+static long raw_mismatch_total = 0, raw_mismatch_big = 0, mul_mismatch_total = 0;
 
 static long check_scale(float s, uint16_t amax_bits, int weight_path)
 {
-    long bad = 0, raw = 0, raw_big = 0;
+    long bad = 0, raw = 0, raw_big = 0, bad_mul = 0;
     float r = 1.0f / s;
     for (uint32_t h = 0; h <= amax_bits; ++h) {
         for (int sg = 0; sg < 2; ++sg) {
@@ -55,7 +59,12 @@ static long check_scale(float s, uint16_t amax_bits, int weight_path)
                 if (fabsf(want) >= 0x1p-26f) ++raw_big;
             }
             if (weight_path) {
-                want = b2f(f2b(want));
+                /* the weight path stores bf16(quotient) and both operands are bf16:
+                 * there the kernels use the single multiply x * r, whose bf16
+                 * rounding must equal that of the IEEE quotient, bit for bit */
+                const uint16_t wb = f2b(want), mb = f2b(x * r);
+                if (wb != mb) ++bad_mul;
+                want = b2f(wb);
                 q = b2f(f2b(q));
             }
             if (oracle_e4m3_from_f32(want) != oracle_e4m3_from_f32(q)) ++bad;
@@ -65,6 +74,8 @@ static long check_scale(float s, uint16_t amax_bits, int weight_path)
     raw_mismatch_total += raw;
 #pragma omp atomic
     raw_mismatch_big += raw_big;
+#pragma omp atomic
+    mul_mismatch_total += bad_mul;
     return bad;
 }
 
@@ -83,5 +94,6 @@ int main(void)
     printf("code mismatches: activation %ld, weight %ld\n", bad_act, bad_w);
     printf("raw binary32 quotient mismatches: %ld (of which |q| >= 2^-26: %ld)\n",
            raw_mismatch_total, raw_mismatch_big);
-    return (bad_act + bad_w + raw_mismatch_big) != 0;
+    printf("weight path, single multiply: bf16 mismatches %ld\n", mul_mismatch_total);
+    return (bad_act + bad_w + raw_mismatch_big + mul_mismatch_total) != 0;
 }

@@ -79,13 +79,15 @@ __device__ __forceinline__ int at_row(int k)
 
 // Four bf16 values (two packed words) -> four codes: quotient by the bf16 scale,
 // rounded to bf16 (two per conversion; opaque so the pair stays one
-// instruction), then e4m3.
-__device__ __forceinline__ uint32_t codes4(uint2 v, float s, float r)
+// instruction), then e4m3 straight from the packed bf16. Both operands are
+// bf16, where RN_bf16(x * RN(1/s)) equals RN_bf16(x / s) for every pair
+// (checked exhaustively): one multiply.
+__device__ __forceinline__ uint32_t codes4(uint2 v, float r)
 {
-    uint32_t q01 = pack_bf16x2(div_by_scale(bf16_lo(v.x), s, r), div_by_scale(bf16_hi(v.x), s, r));
-    uint32_t q23 = pack_bf16x2(div_by_scale(bf16_lo(v.y), s, r), div_by_scale(bf16_hi(v.y), s, r));
+    uint32_t q01 = pack_bf16x2(bf16_lo(v.x) * r, bf16_hi(v.x) * r);
+    uint32_t q23 = pack_bf16x2(bf16_lo(v.y) * r, bf16_hi(v.y) * r);
     asm volatile("" : "+v"(q01), "+v"(q23));
-    return pack_e4m3x4(bf16_lo(q01), bf16_hi(q01), bf16_lo(q23), bf16_hi(q23));
+    return pack_e4m3x4_bf16(q01, q23);
 }
 
 __device__ __forceinline__ uint32_t codes4_exact(uint2 v, float s)
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const uint2 v = make_uint2(wm[2 * i], wm[2 * i + 1]);
-                        q[i] = finite ? codes4(v, sb, r) : codes4_exact(v, sb);
+                        q[i] = finite ? codes4(v, r) : codes4_exact(v, sb);
                     }
                     uint2* dq = reinterpret_cast<uint2*>(p.wq + n * p.ldq + k);
                     dq[0] = make_uint2(q[0], q[1]);

@@ -22,30 +22,44 @@ namespace {
 constexpr int kWavesPerBlock = 4;  // rows per workgroup
 constexpr int kLanes = 64;
 
-// Quotient of the quantizers. kWeight selects the weight path's double
-// rounding (binary32 quotient by bf16(scale), rounded to bf16). kExact uses
-// the IEEE division, for the rows whose scale is not finite (a row holding
-// inf or NaN), where the reciprocal form does not apply.
-template <bool kWeight, bool kExact>
+// Quotient of the activation quantizer. kExact uses the IEEE division, for the
+// rows whose scale is not finite (a row holding inf or NaN), where the
+// reciprocal form does not apply.
+template <bool kExact>
 __device__ __forceinline__ float quotient(float x, float s, float r)
 {
-    float q = kExact ? x / s : div_by_scale(x, s, r);
-    return kWeight ? round_bf16(q) : q;
+    return kExact ? x / s : div_by_scale(x, s, r);
 }
 
-// Converts one 16-byte chunk (8 bf16) to 8 codes.
+// Converts one 16-byte chunk (8 bf16) to 8 codes. The weight path rounds the
+// binary32 quotient by bf16(scale) to bf16 first (the reference's bf16 divide);
+// there both operands are bf16, and RN_bf16(x * RN(1/s)) equals RN_bf16(x / s)
+// for every such pair (checked exhaustively), so one multiply replaces the
+// division, two quotients share one bf16 conversion, and the codes are converted
+// from the packed bf16 quotients.
 template <bool kWeight, bool kExact>
 __device__ __forceinline__ uint2 quantize_chunk(uint4 v, float s, float r)
 {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint2 out;
-    out.x = pack_e4m3x4(quotient<kWeight, kExact>(bf16_lo(v.x), s, r),
-                        quotient<kWeight, kExact>(bf16_hi(v.x), s, r),
-                        quotient<kWeight, kExact>(bf16_lo(v.y), s, r),
-                        quotient<kWeight, kExact>(bf16_hi(v.y), s, r));
-    out.y = pack_e4m3x4(quotient<kWeight, kExact>(bf16_lo(v.z), s, r),
-                        quotient<kWeight, kExact>(bf16_hi(v.z), s, r),
-                        quotient<kWeight, kExact>(bf16_lo(v.w), s, r),
-                        quotient<kWeight, kExact>(bf16_hi(v.w), s, r));
+    if (kWeight && !kExact) {
+        uint32_t p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(bf16_lo(w[e]) * r, bf16_hi(w[e]) * r);
+        asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]));   // keep each pair in one conversion
+        out.x = pack_e4m3x4_bf16(p[0], p[1]);
+        out.y = pack_e4m3x4_bf16(p[2], p[3]);
+        return out;
+    }
+    float q[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        q[2 * e] = quotient<kExact>(bf16_lo(w[e]), s, r);
+        q[2 * e + 1] = quotient<kExact>(bf16_hi(w[e]), s, r);
+        if (kWeight) { q[2 * e] = round_bf16(q[2 * e]); q[2 * e + 1] = round_bf16(q[2 * e + 1]); }
+    }
+    out.x = pack_e4m3x4(q[0], q[1], q[2], q[3]);
+    out.y = pack_e4m3x4(q[4], q[5], q[6], q[7]);
     return out;
 }
 
@@ -188,10 +202,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant(
         float q[8];
         if (finite) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = quotient<false, false>(act[c][j], scale, r);
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false>(act[c][j], scale, r);
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = quotient<false, true>(act[c][j], scale, r);
+            for (int j = 0; j < 8; ++j) q[j] = quotient<true>(act[c][j], scale, r);
         }
         yr[idx] = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
     }
@@ -379,10 +393,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
         float q[8];
         if (finite) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = quotient<false, false>(act[c][j], scale, r);
+            for (int j = 0; j < 8; ++j) q[j] = quotient<false>(act[c][j], scale, r);
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = quotient<false, true>(act[c][j], scale, r);
+            for (int j = 0; j < 8; ++j) q[j] = quotient<true>(act[c][j], scale, r);
         }
         yr[idx] = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
     }

@@ -58,6 +58,20 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
     return w;
 }
 
+// Four bf16 values (two packed words, lo|hi<<16 each) -> four e4m3 codes, with
+// no unpacking: v_cvt_scalef32_pk_fp8_bf16 at scale 1.0 (round to nearest even).
+// For finite inputs of magnitude <= 464 the codes equal pack_e4m3x4 of the same
+// values (the conversions differ only beyond that, in overflow handling); the
+// callers pass bf16 quotients of magnitude <= 450.
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_e4m3x4_bf16(uint32_t q01, uint32_t q23)
+{
+    s16x2_t w = {0, 0};
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(w, __builtin_bit_cast(bf16x2_t, q01), 1.0f, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(w, __builtin_bit_cast(bf16x2_t, q23), 1.0f, true);
+    return __builtin_bit_cast(uint32_t, w);
+}
+
 // Packed max of the magnitudes of two bf16 lanes: (bits & 0x7fff) orders the
 // same way as |x| for every non-NaN pattern and puts NaN patterns above inf.
 __device__ __forceinline__ uint32_t absmax_bf16x2(uint32_t acc, uint32_t w)
