@@ -110,6 +110,46 @@ def test_requant_lora_workload(device):
     _check_lora(bits(w0), bits(a), bits(b), scale, device)
 
 
+@pytest.mark.parametrize("r", [64, 19])
+def test_requant_lora_edge_rows(device, r):
+    """Rows with inf / NaN in W or in the LoRA factors, zero and negative-zero rows,
+    subnormal rows, a row whose merge overflows bf16, and rows the update dominates:
+    the scales and codes bit-exact with the oracle's quantization of the kernel's own
+    merged weight, the merged weight within one bf16 ulp (same class where not finite)."""
+    rng = np.random.default_rng(77 + r)
+    N, K = 40, 1024
+    w = rng.standard_normal((N, K), dtype=np.float32) * 0.02
+    a = rng.standard_normal((r, K), dtype=np.float32) * 0.01
+    b = rng.standard_normal((N, r), dtype=np.float32) * 0.01
+    w[0, 5] = np.inf
+    w[1, 700] = np.nan
+    w[2], b[2] = 0.0, 0.0
+    w[3], b[3] = -0.0, 0.0
+    w[4], b[4] = 1e-39, 0.0
+    w[5, 100], b[5] = 3.38e38, 3e37
+    b[6, 3] = np.inf
+    b[7, 0] = np.nan
+    w[8], b[8] = -300.0, 0.0
+    b[10] = 5.0
+    w[11, 1023] = -np.inf
+    w, a, b = (O.bf16_encode(t) for t in (w, a, b))
+    lora = (from_bits(a, device), from_bits(b, device), 1.0)
+    gq, gs, gm = _requant(w, device, lora=lora, merged=True)
+    want_m = O.lora_merge(w, a, b, 1.0)
+    gv, wv, w0 = (O.bf16_decode(t).astype(np.float64) for t in (gm, want_m, w))
+    fin = np.isfinite(wv)
+    assert np.array_equal(np.isnan(gv), np.isnan(wv)), "NaN positions differ"
+    assert np.array_equal(gv[np.isinf(wv)], wv[np.isinf(wv)]), "infinities differ"
+    with np.errstate(invalid="ignore", over="ignore"):
+        tol = _bf16_ulp(np.maximum(np.maximum(np.abs(w0), np.abs(wv - w0)), np.abs(wv)))
+    assert np.all(np.abs(gv - wv)[fin] <= tol[fin])
+    wq, ws = O.quantize_weight(gm)
+    same_scale = (gs.view(np.uint32) == ws.view(np.uint32)) | (np.isnan(gs) & np.isnan(ws))
+    assert same_scale.all(), f"scales differ in rows {np.flatnonzero(~same_scale)}"
+    bad = ~same_codes(gq, wq)
+    assert not bad.any(), f"{bad.sum()} codes differ, rows {np.unique(np.argwhere(bad)[:, 0])}"
+
+
 def test_merge_only_in_place(device):
     """merge_lora_state's in-place update (wq = NULL): W' written over W."""
     from vdn_fp8.lora import merge_into
