@@ -45,9 +45,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
         for (int j = 0; j < kBatch; ++j) {
             const int c = c0 + j * kLanes;
             const bool ok = c < nch;
-            r[j] = (RES && ok) ? rr[c] : make_uint4(0u, 0u, 0u, 0u);
+            r[j] = (RES && ok) ? load_once(rr + c) : make_uint4(0u, 0u, 0u, 0u);
             g[j] = ok ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
-            b[j] = ok ? br[c] : make_uint4(0u, 0u, 0u, 0u);
+            b[j] = ok ? load_once(br + c) : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {

@@ -156,8 +156,10 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
 #pragma unroll
         for (int c = 0; c < kGroups; ++c) {
             const uint32_t off = (uint32_t)((nr * p.ldw + k0 + 64 * c + 16 * g) * 2);
-            t.w[2 * c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
-            t.w[2 * c + 1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16, 0, 0));
+            // pass 1 leaves W in the caches for pass 2, whose read is the last
+            constexpr int pol = MODE == kRowMax ? 0 : kBufferLoadOnce;
+            t.w[2 * c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, pol));
+            t.w[2 * c + 1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16, 0, pol));
         }
         // B operand, raw (the rank mask applies when it is used, so that no
         // wait for these loads lands here)

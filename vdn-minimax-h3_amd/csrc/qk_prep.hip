@@ -103,7 +103,8 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     uint4 v[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c)
-        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((lane + kLanes * c) * 16), 0, 0));
+        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((lane + kLanes * c) * 16), 0,
+                                                                              kBufferLoadOnce));
 
     float w[8];
     if (p.weight) {

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int idx = lane + kLanes * c;
-        v[c] = (idx < nch) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
+        v[c] = (idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
     }
     uint32_t m2 = 0;
 #pragma unroll
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant(
     for (int c = 0; c < CPL; ++c) {
         const int idx = lane + kLanes * c;
         uint4 a = make_uint4(0u, 0u, 0u, 0u), g = a;
-        if (idx < nch) { a = ar[idx]; g = gr[idx]; }
+        if (idx < nch) { a = load_once(ar + idx); g = load_once(gr + idx); }
         const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, gw[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int idx = lane + kLanes * c;
-        v[c] = (idx < nch) ? xr[idx] : make_uint4(0u, 0u, 0u, 0u);
+        v[c] = (idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
     }
     float ss = 0.0f;
 #pragma unroll
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
     for (int c = 0; c < CPL; ++c) {
         const int idx = part * kLanes + lane + kLanes * WPR * c;
         uint4 a = make_uint4(0u, 0u, 0u, 0u), g = a;
-        if (valid && idx < nch) { a = ar[idx]; g = gr[idx]; }
+        if (valid && idx < nch) { a = load_once(ar + idx); g = load_once(gr + idx); }
         const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, gw[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

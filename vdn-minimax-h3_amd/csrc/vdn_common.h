@@ -49,6 +49,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 
 __device__ __forceinline__ float round_bf16(float v) { return bf16_lo(pack_bf16x2(v, 0.0f)); }
 
+// 16-byte load of data read exactly once (activations streamed through a
+// kernel): non-temporal, so the stream does not displace cached lines that are
+// read again (the activation quantizer on [32760, 5120]: 0.080 ms against
+// 0.083 ms with plain loads).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_once(const uint4* p)
+{
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Cache-policy operand of the raw buffer intrinsics for a read-once load.
+constexpr int kBufferLoadOnce = 2;   // nt
+
 // Four binary32 values -> four e4m3 codes in one dword (byte i = value i).
 __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d)
 {
