@@ -137,6 +137,24 @@ def test_gemm_gate_broadcast(device):
     _check(_rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.02), None, device, epilogue="gate", gate=gate)
 
 
+def test_gemm_operands_on_other_devices(device):
+    """A gate table on the host is moved to the GPU (the result equals the on-device call);
+    scales or a residual on the host are refused with ValueError, never passed as pointers."""
+    rng = np.random.default_rng(12)
+    M, N, K = 64, 256, 256
+    f = _linear(_rand(rng, (N, K), 0.02), _rand(rng, (N,), 0.01), device)
+    qx, sx = vdn_fp8.quantize_rows(from_bits(_rand(rng, (M, K), 1.0), device))
+    gate = from_bits(O.bf16_encode(rng.uniform(0, 2, N).astype(np.float32)), device)
+    want = f.forward_quantized(qx, sx, epilogue="gate", gate=gate)
+    got = f.forward_quantized(qx, sx, epilogue="gate", gate=gate.cpu())
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    with pytest.raises(ValueError):
+        f.forward_quantized(qx, sx.cpu())
+    with pytest.raises(ValueError):
+        f.forward_quantized(qx, sx, epilogue="gate", gate=gate, residual=torch.zeros(M, N, dtype=torch.bfloat16))
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 4352, 128), (4352, 4096, 384), (4100, 4356, 256)])
 def test_gemm_many_tiles(device, M, N, K):
     """More 256 x 256 tiles than compute units: each workgroup walks several tiles,

@@ -224,11 +224,14 @@ class Fp8Linear(nn.Module):
         if x_scale.numel() != M or x_scale.dtype != torch.float32:
             raise ValueError("x_scale must be the fp32 [M, 1] rowwise scale (per-tensor scales are "
                              "the sm100 branch, not built for gfx950)")
+        dev = x_fp8.device
+        if x_scale.device != dev or self.weight_fp8.device != dev:
+            raise ValueError(f"x_fp8 ({dev}), x_scale ({x_scale.device}) and the fp8 weight "
+                             f"({self.weight_fp8.device}) must be on one device")
         if x_fp8.stride(1) != 1:
             x_fp8 = x_fp8.contiguous()
         x_fp8 = _aligned16(x_fp8)
         x_scale = _aligned16(x_scale.contiguous())
-        dev = x_fp8.device
         out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
         epi = _EPILOGUES.get(epilogue)
         if epi is None:
@@ -237,13 +240,13 @@ class Fp8Linear(nn.Module):
         if bias is not None:
             if bias.dtype != torch.bfloat16 or bias.numel() != N:
                 raise ValueError("the fused bias must be a bfloat16 [N] tensor")
-            bias = _aligned16(bias.detach().contiguous())
+            bias = _aligned16(bias.detach().to(dev).contiguous())
         g = gi = res = None
         ldgate = ldres = grows = 0
         if epi == _lib.EPI_GATE:
             if gate is None:
                 raise ValueError('epilogue="gate" needs a gate table')
-            g = gate.detach().reshape(-1, N)
+            g = gate.detach().to(dev).reshape(-1, N)
             if g.dtype != torch.bfloat16 or g.stride(1) != 1:
                 g = g.to(torch.bfloat16).contiguous()
             ldgate, grows = g.stride(0), g.shape[0]
@@ -253,6 +256,8 @@ class Fp8Linear(nn.Module):
                     raise ValueError("gate_index must hold one table row per token")
             if residual is not None:
                 res = residual.detach()
+                if res.device != dev:
+                    raise ValueError(f"residual is on {res.device}, the activation on {dev}")
                 if res.shape != (M, N) or res.dtype != torch.bfloat16 or res.stride(1) != 1:
                     raise ValueError("residual must be a bfloat16 [M, N] tensor with unit column stride")
                 ldres = res.stride(0)
