@@ -150,6 +150,37 @@ def test_requant_lora_edge_rows(device, r):
     assert not bad.any(), f"{bad.sum()} codes differ, rows {np.unique(np.argwhere(bad)[:, 0])}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_requant_lora_float_factors(device, dtype):
+    """fp16 / fp32 adapter factors (external LoRA files): the reference's fp32 update
+    bf16((B @ A) * scale) added in bf16 (lora.py:91-92), then the requantization; the
+    merged weight within one bf16 ulp of a float64 restatement, the codes bit-exact with
+    the oracle's quantization of the kernel's merged weight; merge_into the same."""
+    from vdn_fp8.lora import merge_into
+    rng = np.random.default_rng(31)
+    N, K, r, scale = 96, 1024, 16, 0.5
+    w = O.bf16_encode(rng.standard_normal((N, K), dtype=np.float32) * 0.02)
+    a = (rng.standard_normal((r, K)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal((N, r)) * 0.05).astype(np.float32)
+    at, bt = torch.from_numpy(a).to(dtype), torch.from_numpy(b).to(dtype)
+    a64, b64 = at.double().numpy(), bt.double().numpy()
+    d16 = O.bf16_encode(((b64 @ a64) * scale).astype(np.float32))
+    want = O.bf16_encode(O.bf16_decode(w) + O.bf16_decode(d16))
+    w0 = O.bf16_decode(w).astype(np.float64)
+    wv = O.bf16_decode(want).astype(np.float64)
+    tol = _bf16_ulp(np.maximum(np.maximum(np.abs(w0), np.abs(wv - w0)), np.abs(wv)))
+    gq, gs, gm = _requant(w, device, lora=(at.to(device), bt.to(device), scale), merged=True)
+    assert np.all(np.abs(O.bf16_decode(gm).astype(np.float64) - wv) <= tol)
+    assert np.mean(gm != want) <= 2e-3
+    wq, ws = O.quantize_weight(gm)
+    assert np.array_equal(gs.view(np.uint32), ws.view(np.uint32))
+    assert np.all(same_codes(gq, wq))
+    wt = from_bits(w, device)
+    merge_into(wt, at, bt, scale)          # factors on the host: moved by merge_into
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(wt), gm)
+
+
 def test_merge_only_in_place(device):
     """merge_lora_state's in-place update (wq = NULL): W' written over W."""
     from vdn_fp8.lora import merge_into

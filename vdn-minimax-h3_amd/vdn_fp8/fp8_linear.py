@@ -140,9 +140,12 @@ def requantize_weight(weight, lora=None, merged_out=None):
     """bf16 weight [N, K] -> (fp8 codes [N, K], fp32 scale [N]) with the rowwise
     arithmetic of Fp8Linear.__init__ (fp8_linear.py:262-267).
 
-    lora = (A [r, K] bf16, B [N, r] bf16, scale) folds W + bf16(scale * B @ A) in first,
-    as merge_lora_state does (lora.py:91-92), inside the same kernel. merged_out, if
-    given (bf16 [N, K], may be `weight` itself), receives the merged weight."""
+    lora = (A [r, K], B [N, r], scale) folds W + bf16(scale * B @ A) in first, as
+    merge_lora_state does (lora.py:91-92): with bf16 factors inside the same kernel; with
+    factors of another dtype (fp16 / fp32 adapters) the update is the reference's own
+    fp32 product on the GPU (a plain library GEMM), rounded to bf16 and added, and the
+    kernel requantizes the merged weight. merged_out, if given (bf16 [N, K], may be
+    `weight` itself), receives the merged weight."""
     if not weight.is_cuda:
         raise ValueError("the fp8 requantizer is a HIP kernel; the weight must be on the GPU")
     if weight.dim() != 2 or weight.dtype != torch.bfloat16:
@@ -153,16 +156,21 @@ def requantize_weight(weight, lora=None, merged_out=None):
     s = torch.empty(N, device=w.device, dtype=torch.float32)
     a = b = None
     rank, lscale = 0, 1.0
+    if merged_out is not None:
+        if merged_out.shape != (N, K) or merged_out.dtype != torch.bfloat16 or not merged_out.is_contiguous() \
+                or merged_out.device != w.device:
+            raise ValueError("merged_out must be a contiguous bf16 [N, K] tensor on the weight's device")
     if lora is not None:
         a, b, lscale = lora
         a, b = _lora_factor(a, w, "A"), _lora_factor(b, w, "B")
         rank = a.shape[0]
         if a.shape != (rank, K) or b.shape != (N, rank):
             raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
-    if merged_out is not None:
-        if merged_out.shape != (N, K) or merged_out.dtype != torch.bfloat16 or not merged_out.is_contiguous() \
-                or merged_out.device != w.device:
-            raise ValueError("merged_out must be a contiguous bf16 [N, K] tensor on the weight's device")
+        if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+            merged = w + lora_delta(a, b, lscale)
+            if merged_out is not None:
+                merged_out.copy_(merged)
+            return requantize_weight(merged)
     lib = _lib.load()
     _lib.check(lib.vdn_fp8_requantize_weight(_ptr(w), N, K, K, _ptr(a), _ptr(b), rank, float(lscale),
                                              _ptr(q), K, _ptr(s), _ptr(merged_out), _stream(w)),
@@ -171,9 +179,16 @@ def requantize_weight(weight, lora=None, merged_out=None):
 
 
 def _lora_factor(t, w, name):
-    if t.dtype != torch.bfloat16:
-        raise ValueError(f"LoRA factor {name} must be bfloat16 (got {t.dtype})")
+    if t.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"LoRA factor {name} must be bfloat16, float16 or float32 (got {t.dtype})")
     return t.to(w.device).contiguous()
+
+
+def lora_delta(a, b, scale):
+    """bf16(scale * (B.float() @ A.float())): the reference's update (lora.py:91-92) for
+    factors that are not bf16, as an fp32 GEMM on the factors' device (a plain library
+    GEMM; bf16 factors never come here, the requantize kernel forms their product)."""
+    return ((b.to(torch.float32) @ a.to(torch.float32)) * scale).to(torch.bfloat16)
 
 
 class Fp8Linear(nn.Module):

@@ -20,7 +20,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .fp8_linear import (MIN_WIDTH, SKIP_END_BLOCKS, Fp8Linear, _blocks_to_skip, _ptr,
+from .fp8_linear import (MIN_WIDTH, SKIP_END_BLOCKS, Fp8Linear, _blocks_to_skip, _ptr, lora_delta,
                          _stream)
 
 # Original-layout module names -> diffusers names (lora.py:22-30).
@@ -86,18 +86,23 @@ def _pairs(state):
 
 
 def merge_into(weight, a, b, scale=1.0):
-    """weight (bf16 [N, K], on the GPU, contiguous) += bf16(scale * (B @ A)), in place."""
+    """weight (bf16 [N, K], on the GPU, contiguous) += bf16(scale * (B @ A)), in place.
+    bf16 factors go through the HIP kernel; fp16 / fp32 factors (external adapters) take
+    the reference's fp32 product on the GPU, rounded to bf16, then the bf16 add."""
     if not weight.is_cuda or weight.dtype != torch.bfloat16 or weight.dim() != 2 or not weight.is_contiguous():
         raise ValueError("the LoRA merge is a HIP kernel: the weight must be a contiguous bf16 [N, K] GPU tensor")
     for t, nm in ((a, "A"), (b, "B")):
-        if t.dtype != torch.bfloat16:
-            raise ValueError(f"LoRA factor {nm} must be bfloat16 (got {t.dtype})")
+        if t.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise ValueError(f"LoRA factor {nm} must be bfloat16, float16 or float32 (got {t.dtype})")
     a = a.to(weight.device).contiguous()
     b = b.to(weight.device).contiguous()
     N, K = weight.shape
     r = a.shape[0]
     if a.shape != (r, K) or b.shape != (N, r):
         raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        weight.add_(lora_delta(a, b, scale))
+        return weight
     lib = _lib.load()
     _lib.check(lib.vdn_fp8_requantize_weight(_ptr(weight), N, K, K, _ptr(a), _ptr(b), r, float(scale),
                                              None, 0, None, _ptr(weight), _stream(weight)),
