@@ -261,18 +261,18 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
         const int idx = lane + kLanes * c;
         v[c] = (idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
     }
-    float ss = 0.0f;
+    // sum of squares straight from the packed bf16 pairs (v_dot2c_f32_bf16: no
+    // unpacking), four partial sums to keep the chains short
+    float ssp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float lo = bf16_lo(w4[e]), hi = bf16_hi(w4[e]);
-            ss += lo * lo;
-            ss += hi * hi;
-        }
+        for (int e = 0; e < 4; ++e)
+            ssp[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4[e]),
+                                                     __builtin_bit_cast(bf16x2_t, w4[e]), ssp[e], false);
     }
-    ss = wave_sum_f32(ss);
+    float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
     const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
     // Opaque to the optimizer: the second sweep unpacks the bf16 pairs again
     // instead of keeping the first sweep's binary32 copies live (twice the VGPRs).
