@@ -431,24 +431,28 @@ void k_gemm_fp8(GemmArgs p)
                         const int nl = wn * 128 + 32 * t + 8 * q + 4 * fh;
                         const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
                         const float swv[4] = {sw.x, sw.y, sw.z, sw.w};
-                        float v[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = round_bf16(acc[t][u][4 * q + e] * (sxm * swv[e]));
+                        // bf16 GEMM output, then the bf16 bias add: each rounding done
+                        // two values per conversion, the second one's pairs being the
+                        // stored words (opaque, so the compiler keeps the pairs)
+                        uint32_t r01 = pack_bf16x2(acc[t][u][4 * q] * (sxm * swv[0]), acc[t][u][4 * q + 1] * (sxm * swv[1]));
+                        uint32_t r23 = pack_bf16x2(acc[t][u][4 * q + 2] * (sxm * swv[2]), acc[t][u][4 * q + 3] * (sxm * swv[3]));
+                        asm volatile("" : "+v"(r01), "+v"(r23));
                         if (p.bias) {
                             const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
-                            v[0] = round_bf16(v[0] + bf16_lo(b.x)); v[1] = round_bf16(v[1] + bf16_hi(b.x));
-                            v[2] = round_bf16(v[2] + bf16_lo(b.y)); v[3] = round_bf16(v[3] + bf16_hi(b.y));
+                            r01 = pack_bf16x2(bf16_lo(r01) + bf16_lo(b.x), bf16_hi(r01) + bf16_hi(b.x));
+                            r23 = pack_bf16x2(bf16_lo(r23) + bf16_lo(b.y), bf16_hi(r23) + bf16_hi(b.y));
+                            asm volatile("" : "+v"(r01), "+v"(r23));
                         }
                         if (EPI == VDN_FP8_EPI_GELU_TANH) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+                            r01 = pack_bf16x2(gelu_tanh(bf16_lo(r01)), gelu_tanh(bf16_hi(r01)));
+                            r23 = pack_bf16x2(gelu_tanh(bf16_lo(r23)), gelu_tanh(bf16_hi(r23)));
                         }
                         if (EPI == VDN_FP8_EPI_GATE && FAST) {   // broadcast gate row, no residual
                             const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
-                            v[0] *= bf16_lo(gv.x); v[1] *= bf16_hi(gv.x); v[2] *= bf16_lo(gv.y); v[3] *= bf16_hi(gv.y);
+                            r01 = pack_bf16x2(bf16_lo(r01) * bf16_lo(gv.x), bf16_hi(r01) * bf16_hi(gv.x));
+                            r23 = pack_bf16x2(bf16_lo(r23) * bf16_lo(gv.y), bf16_hi(r23) * bf16_hi(gv.y));
                         }
-                        *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) =
-                            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                        *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
                     }
                 // these accumulators start the next tile from zero
                 acc[2 * th][u] = f32x16_t{};
