@@ -687,6 +687,23 @@ void k_gemm_fp8_ktail(GemmArgs p)
 // lockstep). Measured on the QKV and FFN-down shapes; (4, 2) is as good.
 constexpr int kPhaseMod = 2, kPhaseStep = 1;
 
+// Tile order for a shape (random codes, one MI355X, [32760, N, K] of one DiT
+// block): m-tile groups of 4 with the K rotation (QKV N = 15360: 1.91 ms against
+// 1.92-1.96 for groups of 2, 8, 16 or no rotation; FFN-up N = 13824 ties with 8);
+// narrow outputs (N <= 6144, 24 n-tiles) over long rows (K >= 8192) in groups of
+// 2 (FFN-down [32760, 5120, 13824]: 1.665 ms against 1.714 with 4); narrow
+// outputs over short rows in groups of 4 without the rotation (attn-out
+// [32760, 5120, 5120]: 0.670 ms against 0.678).
+__host__ inline void tile_order(int64_t N, int64_t K, int& phase_mod, int& group_m)
+{
+    phase_mod = kPhaseMod;
+    group_m = kGroupM;
+    if (N <= 6144) {
+        if (K >= 8192) group_m = 2;
+        else phase_mod = 0;
+    }
+}
+
 // Compute units of the current device (the persistent kernel's grid), cached per
 // device; 0 if the runtime cannot say.
 
@@ -730,6 +747,7 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
                (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
                (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n,
                kPhaseMod, kPhaseStep, kGroupM};
+    tile_order(N, K, p.k_phase_mod, p.group_m);
     const bool main = (K % mainloop::BK) == 0;
     int64_t blocks = tiles_m * tiles_n;
     if (main) {
