@@ -365,12 +365,14 @@ def main():
         extra["swiglu_quantize_h3"] = {"shape": [M, 2 * 14336], "ms": round(ms, 4),
                                        "GB/s": round(sw_bytes / (ms * 1e-3) / 1e9, 1)}
         del hh
-        # the block's pre-norm (RMSNorm + AdaLN affine, table of 2 rows) fused with the quantizer
+        # the block's pre-norm (RMSNorm + AdaLN affine) fused with the quantizer: one table row
+        # per latent frame (21 frames of 30 x 52 tokens), the rows chosen per token
         g = torch.Generator().manual_seed(6)
+        frames = 21
         nw = (1 + 0.05 * torch.randn(K, generator=g)).to(torch.bfloat16).to(dev)
-        nsc = (0.2 * torch.randn(2, K, generator=g)).to(torch.bfloat16).to(dev)
-        nsh = (0.2 * torch.randn(2, K, generator=g)).to(torch.bfloat16).to(dev)
-        nidx = torch.randint(0, 2, (M,), generator=g).to(torch.int32).to(dev)
+        nsc = (0.2 * torch.randn(frames, K, generator=g)).to(torch.bfloat16).to(dev)
+        nsh = (0.2 * torch.randn(frames, K, generator=g)).to(torch.bfloat16).to(dev)
+        nidx = (torch.arange(M) * frames // M).to(torch.int32).to(dev)
         ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
         extra["pre_norm_quantize"] = {"ms": round(ms, 4),
                                       "GB/s": round(wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9, 1)}
