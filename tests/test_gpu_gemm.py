@@ -130,6 +130,26 @@ def test_gemm_gate_residual(device):
            epilogue="gate", gate=gate, gate_index=gi, residual=res)
 
 
+@pytest.mark.parametrize("M,N,K,epi", [(300, 260, 400, "gelu_tanh"), (300, 512, 208, "gate_rows"),
+                                       (257, 264, 1040, "gate_broadcast"), (130, 516, 144, "gate_rows")])
+def test_gemm_ktail_and_narrow_epilogues(device, M, N, K, epi):
+    """The epilogues on the K % 128 != 0 kernel and on output rows that are not 16-byte
+    multiples (N % 8 != 0: the general, unstaged epilogue)."""
+    print(f"gemm epilogue {epi} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    x, w, b = _rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.05), _rand(rng, (N,), 0.1)
+    if epi == "gelu_tanh":
+        _check(x, w, b, device, epilogue="gelu_tanh")
+    elif epi == "gate_broadcast":
+        gate = O.bf16_encode(rng.uniform(0, 2, N).astype(np.float32))
+        _check(x, w, b, device, epilogue="gate", gate=gate)
+    else:
+        T = 5
+        gate = O.bf16_encode(rng.uniform(0, 2, (T, N)).astype(np.float32))
+        gi = rng.integers(0, T, M).astype(np.int64)
+        _check(x, w, b, device, epilogue="gate", gate=gate, gate_index=gi, residual=_rand(rng, (M, N), 1.0))
+
+
 def test_gemm_gate_broadcast(device):
     rng = np.random.default_rng(10)
     M, N, K = 257, 512, 512
