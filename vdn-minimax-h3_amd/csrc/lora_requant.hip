@@ -33,6 +33,8 @@
 // the codes 16.
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "vdn_common.h"
 
 namespace vdn {
@@ -46,7 +48,18 @@ constexpr int kTileRows = kRowsPerWave * kWaves;   // 64
 constexpr int kTileCols = 256;                      // one stripe
 constexpr int kGroups = kTileCols / 64;             // per lane: 16 consecutive columns of each 64
 
-enum Mode { kRowMax = 0, kQuantize = 1, kMergeOnly = 2 };
+enum Mode { kRowMax = 0, kQuantize = 1, kMergeOnly = 2, kQuantizeMerged = 3 };
+
+// Byte offset past every buffer descriptor used here: a store sent there is dropped.
+constexpr uint32_t kDropped = 0x80000000u;
+
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x2_t u32x2(uint32_t a, uint32_t b) { return i32x2_t{(int)a, (int)b}; }
+__device__ __forceinline__ i32x4_t u32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+{
+    return i32x4_t{(int)a, (int)b, (int)c, (int)d};
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -130,6 +143,8 @@ template <int RP, int MODE, bool BVEC>
 __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
 {
     constexpr int kS = RP + 8;                       // LDS row (one column k) in elements
+    constexpr bool kCodes = MODE == kQuantize || MODE == kQuantizeMerged;
+    constexpr bool kMerged = MODE == kMergeOnly || MODE == kQuantizeMerged;
     __shared__ __attribute__((aligned(16))) uint16_t sAT[kTileCols * kS];
 
     const int tid = threadIdx.x, lane = tid & (kLanes - 1);
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
                     br, (uint32_t)((nr * p.rank + 32 * s + 8 * g) * 2), 0, 0));
         }
         t.mbits = 0u;
-        if (MODE == kQuantize) {
+        if (kCodes) {
             const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)(p.w_scale + n0), 0, (int)(rows * 4), 0x00020000);
             t.mbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)(nr * 4), 0, 0);
@@ -211,7 +226,9 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
     }
 
     auto compute = [&](int rt, const TileRegs<RP>& t) {
-        const int64_t n = (int64_t)rt * kTileRows + nr;
+        const int64_t n0 = (int64_t)rt * kTileRows;
+        const int64_t rows = min(p.N - n0, (int64_t)kTileRows);
+        const int64_t n = n0 + nr;
         const bool nvalid = n < p.N;
         // B operand: lane holds B[n][32 s + 8 g .. +7], zero beyond the rank
         // (rank % 8 == 0 on the vector path: all 8 or none)
@@ -221,28 +238,37 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
             for (int s = 0; s < RP / 32; ++s)
                 bop[s] = (32 * s + 8 * g < p.rank) ? t.b[s] : bf16x8_t{};
         } else {
-            const int64_t n0 = (int64_t)rt * kTileRows;
             const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-                (void*)(p.b + n0 * p.rank), 0, (int)(min(p.N - n0, (int64_t)kTileRows) * p.rank * 2), 0x00020000);
+                (void*)(p.b + n0 * p.rank), 0, (int)(rows * p.rank * 2), 0x00020000);
 #pragma unroll
             for (int s = 0; s < RP / 32; ++s) bop[s] = b_operand_scalar<RP>(p, br, nr, s, g);
         }
         float sb = 0.0f, r = 0.0f;
-        bool finite = true;
-        if (MODE == kQuantize) {
+        bool exact = false;   // some row of the wave has a non-finite scale
+        if (kCodes) {
             // w_scale[n] holds either the row maximum's bf16 magnitude bits (below
             // 2^16) or, once a workgroup of stripe 0 has passed, the reference's
             // scale (binary32 bits of a value >= 1e-12 or NaN: above 2^16). Both
             // give the same scale; stripe 0 stores it, so racing readers agree.
             const float s32 = t.mbits < 0x10000u ? row_scale(bf16_to_f32((uint16_t)t.mbits)) : __uint_as_float(t.mbits);
-            if (stripe == 0 && g == 0 && nvalid) p.w_scale[n] = s32;
+            const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.w_scale + n0), 0, (int)(rows * 4), 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s32), sr,
+                                                  (stripe == 0 && g == 0) ? (uint32_t)(nr * 4) : kDropped, 0, 0);
             sb = round_bf16(s32);
             r = 1.0f / sb;
-            finite = __builtin_isfinite(sb);
+            exact = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(sb)) != 0;
         }
+        // Outputs go through buffer stores whose descriptors cover the tile's
+        // rows; a lane whose columns lie past K sends its stores out of range
+        // (dropped), so no store sits under a branch.
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kCodes ? p.wq + n0 * p.ldq : nullptr), 0, kCodes ? (int)(rows * p.ldq) : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kMerged ? p.w_merged + n0 * p.ldw : nullptr), 0, kMerged ? (int)(rows * p.ldw * 2) : 0, 0x00020000);
         float mx = 0.0f;
-#pragma unroll
-        for (int c = 0; c < kGroups; ++c) {
+        auto group = [&](int c, auto exact_tag) {
+            constexpr bool kExact = decltype(exact_tag)::value;
             const int64_t k = k0 + 64 * c + 16 * g;       // this lane's 16 columns k .. k + 15
             const bool in = nvalid && k < p.K;            // K % 16 == 0: all 16 or none
             f32x4_t acc[4];
@@ -276,39 +302,58 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
                     x[4 * m + e + 1] = bf16_hi(word) + bf16_hi(d);
                 }
             }
-            if (MODE == kRowMax) {
+            if constexpr (MODE == kRowMax) {
                 float gm = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) gm = __builtin_elementwise_maximum(gm, __builtin_fabsf(x[i]));
-                if (in) mx = __builtin_elementwise_maximum(mx, gm);
+                mx = __builtin_elementwise_maximum(mx, in ? gm : 0.0f);
             } else {
-                uint32_t wm[8];
+            uint32_t wm[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    wm[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-                    asm volatile("" : "+v"(wm[i]));
-                }
-                if (in && p.w_merged) {
-                    uint16_t* dst = p.w_merged + n * p.ldw + k;
-                    if (p.wm16) {
-                        reinterpret_cast<uint4*>(dst)[0] = make_uint4(wm[0], wm[1], wm[2], wm[3]);
-                        reinterpret_cast<uint4*>(dst)[1] = make_uint4(wm[4], wm[5], wm[6], wm[7]);
-                    } else {
+            for (int i = 0; i < 8; ++i) {
+                wm[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+                asm volatile("" : "+v"(wm[i]));
+            }
+            if constexpr (kMerged) {
+                const uint32_t off = in ? (uint32_t)((nr * p.ldw + k) * 2) : kDropped;
+                if (p.wm16) {
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4(wm[0], wm[1], wm[2], wm[3]), mr, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4(wm[4], wm[5], wm[6], wm[7]), mr, off + 16, 0, 0);
+                } else {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) reinterpret_cast<uint2*>(dst)[i] = make_uint2(wm[2 * i], wm[2 * i + 1]);
-                    }
+                    for (int i = 0; i < 4; ++i)
+                        __builtin_amdgcn_raw_buffer_store_b64(u32x2(wm[2 * i], wm[2 * i + 1]), mr, off + 8 * i, 0, 0);
                 }
-                if (MODE == kQuantize && in) {
-                    uint32_t q[4];
+            }
+            if constexpr (kCodes) {
+                uint32_t q[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint2 v = make_uint2(wm[2 * i], wm[2 * i + 1]);
-                        q[i] = finite ? codes4(v, r) : codes4_exact(v, sb);
-                    }
-                    uint2* dq = reinterpret_cast<uint2*>(p.wq + n * p.ldq + k);
-                    dq[0] = make_uint2(q[0], q[1]);
-                    dq[1] = make_uint2(q[2], q[3]);
+                for (int i = 0; i < 4; ++i) {
+                    const uint2 v = make_uint2(wm[2 * i], wm[2 * i + 1]);
+                    q[i] = kExact ? codes4_exact(v, sb) : codes4(v, r);
                 }
+                const uint32_t off = in ? (uint32_t)(nr * p.ldq + k) : kDropped;
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2(q[0], q[1]), qr, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2(q[2], q[3]), qr, off + 8, 0, 0);
+            }
+            }
+        };
+        // One uniform branch per tile: the rows of a wave either all have finite
+        // scales (one multiply per quotient) or take the IEEE division throughout
+        // (the same codes where the scale is finite).
+        // (Scheduling barriers between the groups keep the compiler from hoisting
+        // several groups' work at once, which would cost occupancy.)
+        if (kCodes && exact) {
+#pragma unroll
+            for (int c = 0; c < kGroups; ++c) {
+                group(c, std::true_type{});
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < kGroups; ++c) {
+                group(c, std::false_type{});
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (MODE == kRowMax) {
@@ -382,10 +427,16 @@ void launch_rp(const Args& p, bool merge_only, int cus, hipStream_t st)
         return;
     }
     const dim3 vgrid((unsigned)((p.N + 255) / 256)), vblock(256);
-    const dim3 g1 = stripe_grid<RP, kRowMax, BVEC>(p, cus), g2 = stripe_grid<RP, kQuantize, BVEC>(p, cus);
+    const dim3 g1 = stripe_grid<RP, kRowMax, BVEC>(p, cus);
     hipLaunchKernelGGL(k_zero_u32, vgrid, vblock, 0, st, reinterpret_cast<uint32_t*>(p.w_scale), p.N);
     hipLaunchKernelGGL((k_lora_stripes<RP, kRowMax, BVEC>), g1, block, 0, st, p);
-    hipLaunchKernelGGL((k_lora_stripes<RP, kQuantize, BVEC>), g2, block, 0, st, p);
+    if (p.w_merged) {
+        const dim3 g2 = stripe_grid<RP, kQuantizeMerged, BVEC>(p, cus);
+        hipLaunchKernelGGL((k_lora_stripes<RP, kQuantizeMerged, BVEC>), g2, block, 0, st, p);
+    } else {
+        const dim3 g2 = stripe_grid<RP, kQuantize, BVEC>(p, cus);
+        hipLaunchKernelGGL((k_lora_stripes<RP, kQuantize, BVEC>), g2, block, 0, st, p);
+    }
 }
 
 }  // namespace
@@ -402,7 +453,8 @@ int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, co
     if (w_merged && ((uintptr_t)w_merged % 8)) return set_error(VDN_FP8_EINVAL, "requantize_weight: w_merged must be 8-byte aligned");
     if (wq && (((uintptr_t)wq % 8) || (ldq % 8))) return set_error(VDN_FP8_EINVAL, "requantize_weight: wq rows must be 8-byte aligned");
     if (w_scale && ((uintptr_t)w_scale % 4)) return set_error(VDN_FP8_EINVAL, "requantize_weight: w_scale must be 4-byte aligned");
-    if ((int64_t)kTileRows * ldw * 2 > 0x7fffffffLL || (rank + 33) * K * 2 > 0x7fffffffLL)
+    if ((int64_t)kTileRows * ldw * 2 > 0x7fffffffLL || (rank + 33) * K * 2 > 0x7fffffffLL ||
+        (wq && (int64_t)kTileRows * ldq > 0x7fffffffLL))
         return set_error(VDN_FP8_EINVAL, "requantize_weight: rows too long for the LoRA path");
     if ((N + kTileRows - 1) / kTileRows > (1 << 24) || (K + kTileCols - 1) / kTileCols > (1 << 16))
         return set_error(VDN_FP8_EINVAL, "requantize_weight: shape [%lld, %lld] too large for the LoRA path",
