@@ -57,14 +57,15 @@ def test_quantize_rows_edge_rows(device):
     _check(x, device)
 
 
-def test_quantize_rows_nonfinite(device):
+@pytest.mark.parametrize("K,col", [(64, 3), (5120, 600), (5120, 5119)])
+def test_quantize_rows_nonfinite(device, K, col):
     """A row with inf gets scale inf and signed-zero codes for its finite elements; a
-    row with NaN gets a NaN scale and NaN codes (sign of NaN codes unspecified)."""
-    K = 64
+    row with NaN gets a NaN scale and NaN codes (sign of NaN codes unspecified). At
+    K = 5120 two waves share a row; column 600 lies in the second wave's chunks."""
     x = np.ones((3, K), np.float32)
-    x[0, 3] = np.inf
-    x[1, 4] = -np.inf
-    x[2, 5] = np.nan
+    x[0, col] = np.inf
+    x[1, col - 1] = -np.inf
+    x[2, col - 2] = np.nan
     xb = O.bf16_encode(x)
     gy, gs = _run(xb, device)
     wy, ws = O.quantize_rows(xb)

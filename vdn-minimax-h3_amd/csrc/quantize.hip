@@ -63,23 +63,33 @@ __device__ __forceinline__ uint2 quantize_chunk(uint4 v, float s, float r)
     return out;
 }
 
-// CPL = 16-byte chunks held per lane; the row has K/8 chunks, CPL*64 >= K/8.
-template <int CPL, bool kWeight>
+// WPR waves share a row (1 or 2); CPL = 16-byte chunks held per lane, with
+// CPL*64*WPR >= K/8. Wave part p of a row holds chunks p*64 + lane + 64*WPR*c,
+// so the waves of a row read interleaved 1 KiB blocks; their row maxima meet in
+// LDS. Two waves per row halve the registers per wave and double the
+// workgroups: [32760, 5120] activations in 0.075 ms against 0.077 ms with one
+// (non-temporal loads in both).
+template <int CPL, bool kWeight, int WPR>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
     uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
 {
-    const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
-    if (row >= M) return;
+    static_assert(WPR == 1 || WPR == 2, "one or two waves per row");
+    __shared__ uint32_t smax[kWavesPerBlock];
+    const int lane = threadIdx.x & (kLanes - 1), wave = threadIdx.x / kLanes;
+    const int part = wave % WPR;
+    const int64_t row = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
+    if (WPR == 1 && row >= M) return;
+    // (with two waves per row every wave reaches the barrier below)
+    const bool valid = row < M;
     const int nch = (int)(K >> 3);
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    const uint4* xr = reinterpret_cast<const uint4*>(x + (valid ? row : 0) * ldx);
 
     uint4 v[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int idx = lane + kLanes * c;
-        v[c] = (idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
+        const int idx = part * kLanes + lane + kLanes * WPR * c;
+        v[c] = (valid && idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
     }
     uint32_t m2 = 0;
 #pragma unroll
@@ -89,24 +99,30 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
         m2 = absmax_bf16x2(m2, v[c].z);
         m2 = absmax_bf16x2(m2, v[c].w);
     }
-    const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    if (WPR > 1) {
+        if (lane == 0) smax[wave] = mbits;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
+    }
     const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
-    if (lane == 0) scale_out[row] = scale;
+    if (valid && part == 0 && lane == 0) scale_out[row] = scale;
     const float sdiv = kWeight ? round_bf16(scale) : scale;
     const float r = 1.0f / sdiv;
 
-    uint2* yr = reinterpret_cast<uint2*>(y + row * ldy);
+    uint2* yr = reinterpret_cast<uint2*>(y + (valid ? row : 0) * ldy);
     if (__builtin_isfinite(sdiv)) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + kLanes * c;
-            if (idx < nch) yr[idx] = quantize_chunk<kWeight, false>(v[c], sdiv, r);
+            const int idx = part * kLanes + lane + kLanes * WPR * c;
+            if (valid && idx < nch) yr[idx] = quantize_chunk<kWeight, false>(v[c], sdiv, r);
         }
     } else {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + kLanes * c;
-            if (idx < nch) yr[idx] = quantize_chunk<kWeight, true>(v[c], sdiv, r);
+            const int idx = part * kLanes + lane + kLanes * WPR * c;
+            if (valid && idx < nch) yr[idx] = quantize_chunk<kWeight, true>(v[c], sdiv, r);
         }
     }
 }
@@ -402,13 +418,34 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
     }
 }
 
+// Rows of 4096..16384 elements: two waves per row (chunks per wave rounded up to
+// an instantiated CPL). Returns false for other widths.
+template <bool kWeight>
+bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
+                          uint8_t* y, int64_t ldy, float* s)
+{
+    const int64_t nch = K / 8;
+    if (nch < 8 * kLanes || nch > 2 * 16 * kLanes) return false;
+    const int64_t per = (nch + 2 * kLanes - 1) / (2 * kLanes);     // chunks per lane
+    const dim3 grid((unsigned)((M + 1) / 2)), block(kWavesPerBlock * kLanes);
+#define VDN_CASE(n)                                                                                    \
+    if (per <= n) {                                                                                    \
+        hipLaunchKernelGGL((k_rowquant<n, kWeight, 2>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        return true;                                                                                   \
+    }
+    VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8) VDN_CASE(10) VDN_CASE(12) VDN_CASE(14) VDN_CASE(16)
+#undef VDN_CASE
+    return false;
+}
+
 template <bool kWeight>
 void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t K,
                      int64_t ldx, uint8_t* y, int64_t ldy, float* s)
 {
+    if (launch_rowquant_pair<kWeight>(st, x, M, K, ldx, y, ldy, s)) return;
     const dim3 block(kWavesPerBlock * kLanes);
 #define VDN_CASE(n)                                                                           \
-    case n: hipLaunchKernelGGL((k_rowquant<n, kWeight>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+    case n: hipLaunchKernelGGL((k_rowquant<n, kWeight, 1>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
         return;
     switch (cpl) {
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
