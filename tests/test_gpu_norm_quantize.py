@@ -59,7 +59,7 @@ def test_pre_quantize_plain(device, M, K):
     _check(_rand(rng, (M, K), 1.5), device)
 
 
-@pytest.mark.parametrize("M,K,T", [(256, 5120, 1), (300, 5376, 6), (40, 7168, 3)])
+@pytest.mark.parametrize("M,K,T", [(256, 5120, 1), (300, 5376, 6), (40, 7168, 3), (3, 2048, 2), (9, 14336, 4)])
 def test_pre_quantize_weight_and_table(device, M, K, T):
     rng = np.random.default_rng(M * K + T)
     x = _rand(rng, (M, K), 1.0)

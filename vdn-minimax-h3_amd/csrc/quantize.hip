@@ -19,7 +19,7 @@
 namespace vdn {
 namespace {
 
-constexpr int kWavesPerBlock = 4;  // rows per workgroup
+constexpr int kWavesPerBlock = 4;  // waves per workgroup
 constexpr int kLanes = 64;
 
 // Quotient of the activation quantizer. kExact uses the IEEE division, for the
@@ -255,27 +255,62 @@ __device__ __forceinline__ float wave_sum_f32(float v)
     return v;
 }
 
-// One wave per row, the row in VGPRs:
+// WPR waves per row (1, 2 or 4), the row in VGPRs:
 //   rstd   = 1 / sqrt(sum_k x^2 / K + eps)                       (binary32)
 //   n[k]   = bf16(((x[k] * rstd) * w[k]) * (1 + scale[i][k]) + shift[i][k])
 //   y, s   = the quantize_rows arithmetic on n
 // with i = mod_index[row] (clamped into the table). The affine chain is held in
 // binary32 and rounded once, as the compiled `pre` of fused_block.py does; the
-// codes follow from the bf16 n exactly as quantize_rows' do.
-template <int CPL>
+// codes follow from the bf16 n exactly as quantize_rows' do. Wave part p of a
+// row holds chunks p*64 + lane + 64*WPR*c; the partial sums of squares and the
+// row maxima of the waves of a row meet in LDS (summed in part order, so every
+// wave of the row gets the same rstd). The weight and table chunks are loaded
+// with the row, before the reductions, so their latency hides behind them.
+template <int CPL, int WPR>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs p)
 {
-    const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
-    if (row >= p.M) return;
+    static_assert(kWavesPerBlock % WPR == 0, "rows per workgroup");
+    __shared__ float ssum[kWavesPerBlock];
+    __shared__ uint32_t smax[kWavesPerBlock];
+    // (the wave index as a uniform value: the row and its table index then live in
+    // scalar registers, and the index is read by a scalar load)
+    const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int part = wave % WPR;
+    const int64_t row = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
+    if (WPR == 1 && row >= p.M) return;
+    const bool valid = row < p.M;                    // (WPR > 1: every wave reaches the barriers)
+    const int64_t rr = valid ? row : 0;
     const int nch = (int)(p.K >> 3);
-    const uint4* xr = reinterpret_cast<const uint4*>(p.x + row * p.ldx);
-
+    // Buffer loads: chunks past K (and every chunk of a row past M) fall outside the
+    // descriptor's range and read as zeros, with no branch, so the loads of a row
+    // are in flight together (a conditional plain load here made the compiler wait
+    // for each one before issuing the next).
+    const int rowbytes = nch * 16;
+    int64_t ti = 0;
+    if (p.mod_index) ti = min(max((int64_t)p.mod_index[rr], (int64_t)0), p.mod_rows - 1);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.x + rr * p.ldx), 0, valid ? rowbytes : 0, 0x00020000);
     uint4 v[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int idx = lane + kLanes * c;
-        v[c] = (idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t off = (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u;
+        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, kBufferLoadOnce));
+    }
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.weight ? p.weight : p.x), 0, p.weight ? rowbytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t scs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.mod_scale ? p.mod_scale + ti * p.ldmod : p.x), 0, p.mod_scale ? rowbytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t shs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.mod_shift ? p.mod_shift + ti * p.ldmod : p.x), 0, p.mod_shift ? rowbytes : 0, 0x00020000);
+    const uint4 one = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // 1.0
+    uint4 wv[CPL], sc[CPL], sh[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t off = (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u;
+        wv[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+        if (!p.weight) wv[c] = one;
+        sc[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(scs, off, 0, 0));
+        sh[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(shs, off, 0, 0));
     }
     // sum of squares straight from the packed bf16 pairs (v_dot2c_f32_bf16: no
     // unpacking), four partial sums to keep the chains short
@@ -289,28 +324,25 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
                                                      __builtin_bit_cast(bf16x2_t, w4[e]), ssp[e], false);
     }
     float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
+    if (WPR > 1) {
+        if (lane == 0) ssum[wave] = ss;
+        __syncthreads();
+        ss = ssum[(wave / WPR) * WPR];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) ss += ssum[(wave / WPR) * WPR + w];
+    }
     const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
     // Opaque to the optimizer: the second sweep unpacks the bf16 pairs again
     // instead of keeping the first sweep's binary32 copies live (twice the VGPRs).
 #pragma unroll
     for (int c = 0; c < CPL; ++c) asm volatile("" : "+v"(v[c].x), "+v"(v[c].y), "+v"(v[c].z), "+v"(v[c].w));
 
-    int64_t ti = 0;
-    if (p.mod_index) ti = min(max((int64_t)p.mod_index[row], (int64_t)0), p.mod_rows - 1);
-    const uint4* wr = reinterpret_cast<const uint4*>(p.weight);
-    const uint4* scr = reinterpret_cast<const uint4*>(p.mod_scale + ti * p.ldmod);
-    const uint4* shr = reinterpret_cast<const uint4*>(p.mod_shift + ti * p.ldmod);
     uint32_t m2 = 0;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int idx = lane + kLanes * c;
-        if (idx >= nch) continue;
         const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-        uint4 wv = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // 1.0
-        uint4 sc = make_uint4(0u, 0u, 0u, 0u), sh = sc;
-        if (p.weight) wv = wr[idx];
-        if (p.mod_scale) { sc = scr[idx]; sh = shr[idx]; }
-        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, sw[4] = {sc.x, sc.y, sc.z, sc.w}, hw[4] = {sh.x, sh.y, sh.z, sh.w};
+        const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+        const uint32_t sw[4] = {sc[c].x, sc[c].y, sc[c].z, sc[c].w}, hw[4] = {sh[c].x, sh[c].y, sh[c].z, sh[c].w};
         uint32_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -322,31 +354,38 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
             }
             o[e] = pack_bf16x2(a, b);
         }
+        // chunks past K hold zeros (x = 0, shift = 0): they add nothing to the maximum
         v[c] = make_uint4(o[0], o[1], o[2], o[3]);
         m2 = absmax_bf16x2(m2, v[c].x);
         m2 = absmax_bf16x2(m2, v[c].y);
         m2 = absmax_bf16x2(m2, v[c].z);
         m2 = absmax_bf16x2(m2, v[c].w);
     }
-    uint4* nr = reinterpret_cast<uint4*>(p.normed + row * p.ldn);
+    uint4* nr = reinterpret_cast<uint4*>(p.normed + rr * p.ldn);
     if (!p.y) {                                      // the pre-norm alone (bf16 out)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + kLanes * c;
-            if (idx < nch) nr[idx] = v[c];
+            const int idx = part * kLanes + lane + kLanes * WPR * c;
+            if (valid && idx < nch) nr[idx] = v[c];
         }
         return;
     }
-    const uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+    if (WPR > 1) {
+        if (lane == 0) smax[wave] = mbits;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
+    }
     const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
-    if (lane == 0) p.y_scale[row] = scale;
+    if (valid && part == 0 && lane == 0) p.y_scale[row] = scale;
     const float r = 1.0f / scale;
-    uint2* yr = reinterpret_cast<uint2*>(p.y + row * p.ldy);
+    uint2* yr = reinterpret_cast<uint2*>(p.y + rr * p.ldy);
     const bool finite = __builtin_isfinite(scale);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int idx = lane + kLanes * c;
-        if (idx >= nch) continue;
+        const int idx = part * kLanes + lane + kLanes * WPR * c;
+        if (!valid || idx >= nch) continue;
         if (p.normed) nr[idx] = v[c];
         yr[idx] = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
     }
@@ -515,6 +554,27 @@ extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K,
     return check_launch("swiglu_quantize_rows");
 }
 
+namespace vdn {
+namespace {
+// k_norm_quant with WPR waves per row, chunks per lane rounded up to an
+// instantiated count (2..8); false when none covers the row.
+template <int WPR>
+bool launch_norm_multi(int64_t nch, int64_t M, const NormArgs& p, hipStream_t st)
+{
+    const int64_t per = (nch + WPR * kLanes - 1) / (WPR * kLanes);
+    const dim3 grid((unsigned)((M + kWavesPerBlock / WPR - 1) / (kWavesPerBlock / WPR))), block(kWavesPerBlock * kLanes);
+#define VDN_CASE(n)                                                                 \
+    if (per <= n) {                                                                 \
+        hipLaunchKernelGGL((k_norm_quant<n, WPR>), grid, block, 0, st, p);          \
+        return true;                                                                \
+    }
+    VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
+#undef VDN_CASE
+    return false;
+}
+}  // namespace
+}  // namespace vdn
+
 extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, int64_t ldx, const void* weight,
                                           float eps, const void* mod_scale, const void* mod_shift, int64_t ldmod,
                                           const int32_t* mod_index, int64_t mod_rows, void* y, int64_t ldy,
@@ -539,11 +599,22 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     if (nch > 32 * kLanes) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: K=%lld above the supported 16384", (long long)K);
     NormArgs p{(const uint16_t*)x, M, K, ldx, (const uint16_t*)weight, eps, (const uint16_t*)mod_scale,
                (const uint16_t*)mod_shift, ldmod, mod_index, mod_rows, (uint8_t*)y, ldy, y_scale, (uint16_t*)normed, ldn};
-    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    const dim3 block(kWavesPerBlock * kLanes);
+    if (nch > 4 * kLanes) {
+        // rows of more than 2048 elements: two waves per row up to 8192 elements,
+        // four beyond (at most 8 chunks per lane: the weight and table chunks are
+        // held in registers with the row)
+        if (nch <= 16 * kLanes) {
+            if (launch_norm_multi<2>(nch, M, p, stream)) return check_launch("norm_quantize_rows");
+        } else if (launch_norm_multi<4>(nch, M, p, stream)) {
+            return check_launch("norm_quantize_rows");
+        }
+        return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
+    }
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
     switch (pick_cpl(nch)) {
-#define VDN_CASE(n) case n: hipLaunchKernelGGL(k_norm_quant<n>, grid, block, 0, stream, p); break;
-        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
-        VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
+#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_norm_quant<n, 1>), grid, block, 0, stream, p); break;
+        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4)
 #undef VDN_CASE
         default: return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
     }
