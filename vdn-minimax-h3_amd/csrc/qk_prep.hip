@@ -41,22 +41,20 @@ struct QkArgs {
     int64_t ldo;
 };
 
-// Eight table values for elements i0 .. i0 + 7 of row t, rounded to bf16 and
-// returned as binary32.
-__device__ __forceinline__ void load_table8(const QkArgs& p, const void* tab, int64_t t, int i0, float v[8])
+// Eight table values for elements i0 .. i0 + 7 of one row, rounded to bf16 and
+// returned as binary32, from the 32 bytes at the row's element i0 (binary32
+// tables use both halves, bf16 tables the first).
+__device__ __forceinline__ void decode_table8(uint4 lo, uint4 hi, bool bf16, float v[8])
 {
-    if (p.cs_bf16) {
-        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(tab) + t * p.ldcs + i0);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    if (bf16) {
+        const uint32_t w[4] = {lo.x, lo.y, lo.z, lo.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(w[e]); v[2 * e + 1] = bf16_hi(w[e]); }
     } else {
-        const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(tab) + t * p.ldcs + i0);
-        const float4 a = f[0], b = f[1];
-        const float raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t raw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            const uint32_t r = pack_bf16x2(raw[e], raw[e + 1]);
+            const uint32_t r = pack_bf16x2(__uint_as_float(raw[e]), __uint_as_float(raw[e + 1]));
             v[e] = bf16_lo(r);
             v[e + 1] = bf16_hi(r);
         }
@@ -91,7 +89,8 @@ template <int G, int CPL>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
 {
     const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    // the token as a uniform value: its row bases live in scalar registers
+    const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     if (t >= p.T) return;
     const int nch = (int)(p.H * G);                  // chunks per token
     const int j = lane % G;                           // chunk index inside the head
@@ -106,15 +105,34 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
         v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((lane + kLanes * c) * 16), 0,
                                                                               kBufferLoadOnce));
 
+    // The weight and the token's cos/sin values, likewise by buffer loads issued
+    // with the token's (an absent weight and the elements past the rotary
+    // dimension fall outside their descriptors; no branch, so no load waits for
+    // another before it is issued).
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.weight ? p.weight : p.x), 0, p.weight ? (int)(p.d * 2) : 0, 0x00020000);
+    const uint4 wq = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)(i0 * 2), 0, 0));
+    const int esz = p.cs_bf16 ? 2 : 4;
+    const int cbytes = p.R > 0 ? (int)(p.R * esz) : 0;
+    const int64_t crow = t * p.ldcs * esz;
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.R > 0 ? static_cast<const uint8_t*>(p.cos) + crow : reinterpret_cast<const uint8_t*>(p.x)), 0, cbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.R > 0 ? static_cast<const uint8_t*>(p.sin) + crow : reinterpret_cast<const uint8_t*>(p.x)), 0, cbytes, 0x00020000);
+    const uint32_t coff = (uint32_t)(i0 * esz);
+    const uint4 c0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cr, coff, 0, 0));
+    const uint4 c1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cr, coff + 16, 0, 0));
+    const uint4 s0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, coff, 0, 0));
+    const uint4 s1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, coff + 16, 0, 0));
+
     float w[8];
-    if (p.weight) {
-        const uint4 q = *reinterpret_cast<const uint4*>(p.weight + i0);
-        const uint32_t ww[4] = {q.x, q.y, q.z, q.w};
+    {
+        const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { w[2 * e] = bf16_lo(ww[e]); w[2 * e + 1] = bf16_hi(ww[e]); }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w[e] = 1.0f;
+        for (int e = 0; e < 4; ++e) {
+            w[2 * e] = p.weight ? bf16_lo(ww[e]) : 1.0f;
+            w[2 * e + 1] = p.weight ? bf16_hi(ww[e]) : 1.0f;
+        }
     }
     const int half = (int)(p.R / 2);
     const bool rot = i0 < p.R;                        // R % 16 == 0: whole chunks rotate or pass
@@ -122,12 +140,12 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     const int partner = lane + (first ? half / 8 : -(half / 8));
     const bool full_rot = p.R == p.d;                 // uniform
     float cs[8], sn[8];
-    if (rot) {
-        load_table8(p, p.cos, t, i0, cs);
-        load_table8(p, p.sin, t, i0, sn);
-    } else {
+    decode_table8(c0, c1, p.cs_bf16, cs);
+    decode_table8(s0, s1, p.cs_bf16, sn);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { cs[e] = 1.0f; sn[e] = 0.0f; }
+    for (int e = 0; e < 8; ++e) {
+        cs[e] = rot ? cs[e] : 1.0f;
+        sn[e] = rot ? sn[e] : 0.0f;
     }
 
     uint16_t* orow = p.out + t * p.ldo;
