@@ -30,7 +30,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
     uint16_t* out, int64_t ldo, int64_t M, int64_t N)   // out may alias residual or branch
 {
     const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t m = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    // the row as a uniform value: its gate index is read by a scalar load, which the
+    // row's vector loads do not have to wait behind
+    const int64_t m = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     if (m >= M) return;
     int64_t gi = 0;
     if (gate_index) gi = min(max((int64_t)gate_index[m], (int64_t)0), gate_rows - 1);
