@@ -147,3 +147,37 @@ def test_swiglu_quantize(device, M, K):
     diff = np.abs(gy.astype(np.int32) - wy.astype(np.int32))
     assert np.mean(gy != wy) < 1e-3, "more than 0.1% of codes differ"
     assert np.all((diff <= 1) | (np.abs(gv - wv) <= 0.07 * np.abs(wv) + 1e-30)), "a code is off by more than one step"
+
+
+def test_quantize_rows_large_output(device):
+    """An output beyond the last-level cache (>= 256 MiB of codes: the non-temporal store
+    path) is bit-identical to quantizing the same rows in small batches (the cached store
+    path), and sampled rows match the oracle."""
+    M, K = 20000, 13824
+    print(f"quantize_rows large M={M} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(5)
+    x = torch.randn(M, K, device=device, generator=g).to(torch.bfloat16)
+    y, s = vdn_fp8.quantize_rows(x)
+    for r0 in range(0, M, 4000):
+        yb, sb = vdn_fp8.quantize_rows(x[r0:r0 + 4000])
+        assert torch.equal(y[r0:r0 + 4000].view(torch.uint8), yb.view(torch.uint8)), f"rows {r0}.. differ"
+        assert torch.equal(s[r0:r0 + 4000].view(torch.int32), sb.view(torch.int32))
+    rows = torch.arange(3, M, 1999, device=device)
+    xs = bits(x[rows])
+    wy, ws = O.quantize_rows(xs)
+    assert np.all(same_codes(codes(y[rows]), wy))
+    assert np.array_equal(s[rows].cpu().numpy().reshape(-1).view(np.uint32), ws.view(np.uint32))
+
+
+def test_swiglu_quantize_large_output(device):
+    """SwiGLU at the H3 width with an output beyond the last-level cache (non-temporal
+    stores) is bit-identical to the same rows in small batches (cached stores)."""
+    M, K = 19000, 14336
+    print(f"swiglu_quantize large M={M} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(6)
+    h = (2.0 * torch.randn(M, 2 * K, device=device, generator=g)).to(torch.bfloat16)
+    y, s = vdn_fp8.swiglu_quantize(h)
+    for r0 in range(0, M, 4000):
+        yb, sb = vdn_fp8.swiglu_quantize(h[r0:r0 + 4000])
+        assert torch.equal(y[r0:r0 + 4000].view(torch.uint8), yb.view(torch.uint8)), f"rows {r0}.. differ"
+        assert torch.equal(s[r0:r0 + 4000].view(torch.int32), sb.view(torch.int32))
