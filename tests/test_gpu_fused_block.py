@@ -210,3 +210,22 @@ def test_fast_block_forward_bf16_ff(device):
         want = FB.post(h, g2, idx, down(FB._swiglu_ref(proj(n2))))
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_post_large_output(device):
+    """An output beyond the last-level cache (>= 256 MiB: non-temporal stores) equals the
+    same rows done in small batches (cached stores), and sampled rows match the oracle."""
+    M, N, T = 32760, 5120, 3
+    print(f"post large M={M} N={N}", flush=True)
+    g = torch.Generator(device=device).manual_seed(8)
+    r = torch.randn(M, N, device=device, generator=g).to(torch.bfloat16)
+    b = (3 * torch.randn(M, N, device=device, generator=g)).to(torch.bfloat16)
+    gt = (2 * torch.rand(T, N, device=device, generator=g)).to(torch.bfloat16)
+    idx = torch.randint(0, T, (M,), device=device, generator=g)
+    out = FB.post(r, gt, idx, b)
+    for r0 in range(0, M, 8192):
+        ob = FB.post(r[r0:r0 + 8192], gt, idx[r0:r0 + 8192], b[r0:r0 + 8192])
+        assert torch.equal(out[r0:r0 + 8192].view(torch.int16), ob.view(torch.int16)), f"rows {r0}.. differ"
+    rows = torch.arange(7, M, 2731, device=device)
+    want = O.gated_residual(bits(r[rows]), bits(gt), idx[rows].cpu().numpy(), bits(b[rows]))
+    assert np.array_equal(bits(out[rows]), want)

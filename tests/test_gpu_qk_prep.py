@@ -142,3 +142,19 @@ def test_qkv_shares_one_quantization(device):
     assert q.shape == k.shape == v.shape == (T, H, d)
     assert torch.equal(qr, want[0]) and torch.equal(kr, want[1]) and torch.equal(v, want[2]) and vr is v
     assert torch.equal(q, wq) and torch.equal(k, wk)
+
+
+def test_qk_prep_large_output(device):
+    """q of the QKV workload at full size (an output beyond the last-level cache:
+    non-temporal stores) equals the same tokens done in small batches (cached stores)."""
+    T, H, d = 32760, 40, 128
+    print(f"qk_prep large T={T} H={H} d={d}", flush=True)
+    g = torch.Generator(device=device).manual_seed(9)
+    q = torch.randn(T, H, d, device=device, generator=g).to(torch.bfloat16)
+    w = (1 + 0.05 * torch.randn(d, device=device, generator=g)).to(torch.bfloat16)
+    th = torch.rand(T, d // 2, device=device, generator=g) * 6.28
+    cs, sn = torch.cat([th.cos(), th.cos()], 1), torch.cat([th.sin(), th.sin()], 1)
+    out = vdn_fp8.qk_prep(q, w, 1e-6, cs, sn)
+    for t0 in range(0, T, 8192):
+        ob = vdn_fp8.qk_prep(q[t0:t0 + 8192], w, 1e-6, cs[t0:t0 + 8192], sn[t0:t0 + 8192])
+        assert torch.equal(out[t0:t0 + 8192].view(torch.int16), ob.view(torch.int16)), f"tokens {t0}.. differ"

@@ -27,6 +27,11 @@ namespace {
 
 constexpr int kLanes = 64;
 constexpr int kWavesPerBlock = 4;   // tokens per workgroup
+// Outputs of at least this many bytes are stored non-temporally: beyond what the
+// 256 MB last-level cache holds, cached stores only evict each other
+// ([32760, 40, 128]: 0.130 ms against 0.142 ms).
+constexpr int64_t kNtStoreBytes = 256ll << 20;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct QkArgs {
     const uint16_t* x;
@@ -84,8 +89,8 @@ __device__ __forceinline__ float row16_sum(float v)
     return v;
 }
 
-// G = d / 8 lanes per head; CPL = chunks per lane.
-template <int G, int CPL>
+// G = d / 8 lanes per head; CPL = chunks per lane; NT: non-temporal output stores.
+template <int G, int CPL, bool NT>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
 {
     const int lane = threadIdx.x & (kLanes - 1);
@@ -188,9 +193,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
             }
         }
         if (q < nch) {
-            *reinterpret_cast<uint4*>(orow + 8 * q) =
-                make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
-                           pack_bf16x2(o[6], o[7]));
+            const u32x4_t ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                                pack_bf16x2(o[6], o[7])};
+            if (NT) __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(orow + 8 * q));
+            else *reinterpret_cast<u32x4_t*>(orow + 8 * q) = ov;
         }
     }
 }
@@ -199,8 +205,13 @@ template <int G>
 int launch_g(const QkArgs& p, int cpl, hipStream_t stream)
 {
     const dim3 grid((unsigned)((p.T + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    const bool nt = p.T * p.H * p.d * 2 >= kNtStoreBytes;
     switch (cpl) {
-#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_qk_prep<G, n>), grid, block, 0, stream, p); break;
+#define VDN_CASE(n)                                                                      \
+    case n:                                                                              \
+        if (nt) hipLaunchKernelGGL((k_qk_prep<G, n, true>), grid, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((k_qk_prep<G, n, false>), grid, block, 0, stream, p);    \
+        break;
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
         VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
 #undef VDN_CASE
