@@ -229,3 +229,20 @@ def test_post_large_output(device):
     rows = torch.arange(7, M, 2731, device=device)
     want = O.gated_residual(bits(r[rows]), bits(gt), idx[rows].cpu().numpy(), bits(b[rows]))
     assert np.array_equal(bits(out[rows]), want)
+
+
+def test_pre_large_output(device):
+    """The pre-norm alone on [32760, 5120] (a normed output beyond the last-level cache:
+    non-temporal stores) equals the same rows done in small batches (cached stores)."""
+    M, K, T = 32760, 5120, 4
+    print(f"pre large M={M} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(10)
+    x = torch.randn(M, K, device=device, generator=g).to(torch.bfloat16)
+    w = (1 + 0.05 * torch.randn(K, device=device, generator=g)).to(torch.bfloat16)
+    sc = (0.2 * torch.randn(T, K, device=device, generator=g)).to(torch.bfloat16)
+    sh = (0.2 * torch.randn(T, K, device=device, generator=g)).to(torch.bfloat16)
+    idx = torch.randint(0, T, (M,), device=device, generator=g).to(torch.int32)
+    out = FB.pre(x, w, 1e-6, sc, sh, idx)
+    for r0 in range(0, M, 8192):
+        ob = FB.pre(x[r0:r0 + 8192], w, 1e-6, sc, sh, idx[r0:r0 + 8192])
+        assert torch.equal(out[r0:r0 + 8192].view(torch.int16), ob.view(torch.int16)), f"rows {r0}.. differ"

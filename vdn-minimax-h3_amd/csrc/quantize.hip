@@ -21,14 +21,21 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;  // waves per workgroup
 
-// Codes outputs of at least this many bytes are stored non-temporally: beyond what
-// the 256 MB last-level cache holds the cached stores only evict each other
-// ([32760, 13824]: 0.229 ms against 0.251 ms), while smaller outputs stay in that
-// cache for the GEMM that reads them next ([32760, 5120]: 0.084 ms cached, 0.086 ms
-// non-temporal).
+// Outputs (codes, normed rows) of at least this many bytes are stored
+// non-temporally: beyond what the 256 MB last-level cache holds the cached stores
+// only evict each other ([32760, 13824] codes: 0.229 ms against 0.251 ms), while
+// smaller outputs stay in that cache for the kernel that reads them next
+// ([32760, 5120] codes: 0.084 ms cached, 0.086 ms non-temporal).
 constexpr int64_t kNtStoreBytes = 256ll << 20;
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+template <bool NT>
+__device__ __forceinline__ void store_normed(uint4* p, uint4 v)
+{
+    if (NT) __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+    else *p = v;
+}
+
 template <bool NT>
 __device__ __forceinline__ void store_codes(uint2* p, uint2 v)
 {
@@ -281,7 +288,7 @@ __device__ __forceinline__ float wave_sum_f32(float v)
 // row maxima of the waves of a row meet in LDS (summed in part order, so every
 // wave of the row gets the same rstd). The weight and table chunks are loaded
 // with the row, before the reductions, so their latency hides behind them.
-template <int CPL, int WPR>
+template <int CPL, int WPR, bool NT>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs p)
 {
     static_assert(kWavesPerBlock % WPR == 0, "rows per workgroup");
@@ -381,7 +388,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int idx = part * kLanes + lane + kLanes * WPR * c;
-            if (valid && idx < nch) nr[idx] = v[c];
+            if (valid && idx < nch) store_normed<NT>(nr + idx, v[c]);
         }
         return;
     }
@@ -401,7 +408,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
     for (int c = 0; c < CPL; ++c) {
         const int idx = part * kLanes + lane + kLanes * WPR * c;
         if (!valid || idx >= nch) continue;
-        if (p.normed) nr[idx] = v[c];
+        if (p.normed) store_normed<NT>(nr + idx, v[c]);
         yr[idx] = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
     }
 }
@@ -588,11 +595,13 @@ namespace {
 template <int WPR>
 bool launch_norm_multi(int64_t nch, int64_t M, const NormArgs& p, hipStream_t st)
 {
+    const bool nt = p.normed && M * nch * 16 >= kNtStoreBytes;   // the normed bf16 output
     const int64_t per = (nch + WPR * kLanes - 1) / (WPR * kLanes);
     const dim3 grid((unsigned)((M + kWavesPerBlock / WPR - 1) / (kWavesPerBlock / WPR))), block(kWavesPerBlock * kLanes);
 #define VDN_CASE(n)                                                                 \
     if (per <= n) {                                                                 \
-        hipLaunchKernelGGL((k_norm_quant<n, WPR>), grid, block, 0, st, p);          \
+        if (nt) hipLaunchKernelGGL((k_norm_quant<n, WPR, true>), grid, block, 0, st, p);  \
+        else hipLaunchKernelGGL((k_norm_quant<n, WPR, false>), grid, block, 0, st, p);   \
         return true;                                                                \
     }
     VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
@@ -640,7 +649,7 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     }
     const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
     switch (pick_cpl(nch)) {
-#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_norm_quant<n, 1>), grid, block, 0, stream, p); break;
+#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_norm_quant<n, 1, false>), grid, block, 0, stream, p); break;
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4)
 #undef VDN_CASE
         default: return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
