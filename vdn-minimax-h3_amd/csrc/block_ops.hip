@@ -35,18 +35,22 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
     uint16_t* out, int64_t ldo, int64_t M, int64_t N)   // out may alias residual or branch
 {
     const int lane = threadIdx.x & (kLanes - 1);
-    // the row as a uniform value: its gate index is read by a scalar load, which the
-    // row's vector loads do not have to wait behind
-    const int64_t m = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    // One wave per (row, span of kBatch * 64 chunks): every wave issues all its loads
+    // at once and makes one round trip. The unit as a uniform value: the row's gate
+    // index is read by a scalar load, which the vector loads do not wait behind.
+    const int nch = (int)(N >> 3);
+    const int64_t spans = (nch + kBatch * kLanes - 1) / (kBatch * kLanes);
+    const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int64_t m = unit / spans;
     if (m >= M) return;
     int64_t gi = 0;
     if (gate_index) gi = min(max((int64_t)gate_index[m], (int64_t)0), gate_rows - 1);
-    const int nch = (int)(N >> 3);
     const uint4* rr = reinterpret_cast<const uint4*>(residual + m * ldr);
     const uint4* gr = reinterpret_cast<const uint4*>(gate + gi * ldgate);
     const uint4* br = reinterpret_cast<const uint4*>(branch + m * ldb);
     uint4* orow = reinterpret_cast<uint4*>(out + m * ldo);
-    for (int c0 = lane; c0 < nch; c0 += kBatch * kLanes) {
+    {
+        const int c0 = (int)(unit - m * spans) * kBatch * kLanes + lane;
         uint4 r[kBatch], g[kBatch], b[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -85,7 +89,8 @@ int launch_gated_residual(const uint16_t* residual, int64_t ldr, const uint16_t*
                           const int32_t* gate_index, int64_t gate_rows, const uint16_t* branch, int64_t ldb,
                           uint16_t* out, int64_t ldo, int64_t M, int64_t N, hipStream_t stream)
 {
-    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    const int64_t spans = (N / 8 + kBatch * kLanes - 1) / (kBatch * kLanes);   // waves per row
+    const dim3 grid((unsigned)((M * spans + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
     const bool nt = M * N * 2 >= kNtStoreBytes;
 #define VDN_GR(R, T)                                                                                         \
     hipLaunchKernelGGL((k_gated_residual<R, T>), grid, block, 0, stream, residual, ldr, gate, ldgate, gate_index, \
@@ -118,7 +123,7 @@ extern "C" int vdn_fp8_gated_residual(const void* residual, int64_t ldr, const v
     if ((residual && !aligned(residual, 16)) || !aligned(gate, 16) || !aligned(branch, 16) || !aligned(out, 16) ||
         (gate_index && ((uintptr_t)gate_index % 4)))
         return set_error(VDN_FP8_EINVAL, "gated_residual: misaligned pointer (residual, gate, branch, out 16 B)");
-    if (M / kWavesPerBlock >= 0x7fffffffLL || N >= 0x7fffffffLL)
+    if (M * (N / 8 / (kBatch * kLanes) + 1) / kWavesPerBlock >= 0x7fffffffLL || N >= 0x7fffffffLL)
         return set_error(VDN_FP8_EINVAL, "gated_residual: problem too large");
     return launch_gated_residual((const uint16_t*)residual, ldr, (const uint16_t*)gate, ldgate, gate_index, gate_rows,
                                  (const uint16_t*)branch, ldb, (uint16_t*)out, ldo, M, N, stream);
