@@ -308,8 +308,6 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
     // are in flight together (a conditional plain load here made the compiler wait
     // for each one before issuing the next).
     const int rowbytes = nch * 16;
-    int64_t ti = 0;
-    if (p.mod_index) ti = min(max((int64_t)p.mod_index[rr], (int64_t)0), p.mod_rows - 1);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.x + rr * p.ldx), 0, valid ? rowbytes : 0, 0x00020000);
     uint4 v[CPL];
@@ -318,6 +316,11 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs
         const uint32_t off = (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u;
         v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, kBufferLoadOnce));
     }
+    // the row's loads are issued before the table index is read (a scalar load the
+    // table addresses wait for), so they do not wait behind it
+    __builtin_amdgcn_sched_barrier(0);
+    int64_t ti = 0;
+    if (p.mod_index) ti = min(max((int64_t)p.mod_index[rr], (int64_t)0), p.mod_rows - 1);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.weight ? p.weight : p.x), 0, p.weight ? rowbytes : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t scs = __builtin_amdgcn_make_buffer_rsrc(
