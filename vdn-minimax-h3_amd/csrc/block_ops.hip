@@ -26,7 +26,8 @@ constexpr int kBatch = 4;            // chunks per lane in flight
 // 256 MB last-level cache holds, cached stores only evict each other ([32760, 5120]:
 // 0.180 ms against 0.193 ms).
 constexpr int64_t kNtStoreBytes = 256ll << 20;
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kStoreOnce = 2;        // cache policy of a non-temporal buffer store
 
 template <bool RES, bool NT>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
@@ -37,47 +38,52 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
     const int lane = threadIdx.x & (kLanes - 1);
     // One wave per (row, span of kBatch * 64 chunks): every wave issues all its loads
     // at once and makes one round trip. The unit as a uniform value: the row's gate
-    // index is read by a scalar load, which the vector loads do not wait behind.
+    // index is read by a scalar load.
     const int nch = (int)(N >> 3);
     const int64_t spans = (nch + kBatch * kLanes - 1) / (kBatch * kLanes);
     const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int64_t m = unit / spans;
     if (m >= M) return;
+    // Buffer loads and stores over the row (16-byte chunks past N fall outside the
+    // descriptors: zeros read, stores dropped), so nothing sits under a branch and
+    // the stores go out back to back.
+    const int rowbytes = nch * 16;
+    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(RES ? residual + m * ldr : branch), 0, RES ? rowbytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)(branch + m * ldb), 0, rowbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc((void*)(out + m * ldo), 0, rowbytes, 0x00020000);
+    const uint32_t c0 = (uint32_t)(unit - m * spans) * kBatch * kLanes + lane;
+    uint4 r[kBatch], g[kBatch], b[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+        const uint32_t off = (c0 + j * kLanes) * 16u;
+        r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rrs, off, 0, kBufferLoadOnce));
+        b[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(brs, off, 0, kBufferLoadOnce));
+    }
+    // the gate row's index is read after the row's own loads are issued (the gate
+    // addresses wait for it; the residual and branch loads need not)
+    __builtin_amdgcn_sched_barrier(0);
     int64_t gi = 0;
     if (gate_index) gi = min(max((int64_t)gate_index[m], (int64_t)0), gate_rows - 1);
-    const uint4* rr = reinterpret_cast<const uint4*>(residual + m * ldr);
-    const uint4* gr = reinterpret_cast<const uint4*>(gate + gi * ldgate);
-    const uint4* br = reinterpret_cast<const uint4*>(branch + m * ldb);
-    uint4* orow = reinterpret_cast<uint4*>(out + m * ldo);
-    {
-        const int c0 = (int)(unit - m * spans) * kBatch * kLanes + lane;
-        uint4 r[kBatch], g[kBatch], b[kBatch];
+    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc((void*)(gate + gi * ldgate), 0, rowbytes, 0x00020000);
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int c = c0 + j * kLanes;
-            const bool ok = c < nch;
-            r[j] = (RES && ok) ? load_once(rr + c) : make_uint4(0u, 0u, 0u, 0u);
-            g[j] = ok ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
-            b[j] = ok ? load_once(br + c) : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < kBatch; ++j)
+        g[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(grs, (c0 + j * kLanes) * 16u, 0, 0));
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+        const uint32_t rw[4] = {r[j].x, r[j].y, r[j].z, r[j].w}, gw[4] = {g[j].x, g[j].y, g[j].z, g[j].w},
+                       bw[4] = {b[j].x, b[j].y, b[j].z, b[j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // without a residual the product is stored as it is (no + 0: that would turn -0 into +0)
+            float lo = bf16_lo(gw[e]) * bf16_lo(bw[e]);
+            float hi = bf16_hi(gw[e]) * bf16_hi(bw[e]);
+            if (RES) { lo = bf16_lo(rw[e]) + lo; hi = bf16_hi(rw[e]) + hi; }
+            o[e] = pack_bf16x2(lo, hi);
         }
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int c = c0 + j * kLanes;
-            if (c >= nch) continue;
-            const uint32_t rw[4] = {r[j].x, r[j].y, r[j].z, r[j].w}, gw[4] = {g[j].x, g[j].y, g[j].z, g[j].w},
-                           bw[4] = {b[j].x, b[j].y, b[j].z, b[j].w};
-            uint32_t o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // without a residual the product is stored as it is (no + 0: that would turn -0 into +0)
-                float lo = bf16_lo(gw[e]) * bf16_lo(bw[e]);
-                float hi = bf16_hi(gw[e]) * bf16_hi(bw[e]);
-                if (RES) { lo = bf16_lo(rw[e]) + lo; hi = bf16_hi(rw[e]) + hi; }
-                o[e] = pack_bf16x2(lo, hi);
-            }
-            if (NT) __builtin_nontemporal_store(u32x4_t{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4_t*>(orow + c));
-            else orow[c] = make_uint4(o[0], o[1], o[2], o[3]);
-        }
+        __builtin_amdgcn_raw_buffer_store_b128(i32x4_t{(int)o[0], (int)o[1], (int)o[2], (int)o[3]}, ors,
+                                               (c0 + j * kLanes) * 16u, 0, NT ? kStoreOnce : 0);
     }
 }
 
@@ -123,7 +129,7 @@ extern "C" int vdn_fp8_gated_residual(const void* residual, int64_t ldr, const v
     if ((residual && !aligned(residual, 16)) || !aligned(gate, 16) || !aligned(branch, 16) || !aligned(out, 16) ||
         (gate_index && ((uintptr_t)gate_index % 4)))
         return set_error(VDN_FP8_EINVAL, "gated_residual: misaligned pointer (residual, gate, branch, out 16 B)");
-    if (M * (N / 8 / (kBatch * kLanes) + 1) / kWavesPerBlock >= 0x7fffffffLL || N >= 0x7fffffffLL)
+    if (M * (N / 8 / (kBatch * kLanes) + 1) / kWavesPerBlock >= 0x7fffffffLL || N >= 0x40000000LL)
         return set_error(VDN_FP8_EINVAL, "gated_residual: problem too large");
     return launch_gated_residual((const uint16_t*)residual, ldr, (const uint16_t*)gate, ldgate, gate_index, gate_rows,
                                  (const uint16_t*)branch, ldb, (uint16_t*)out, ldo, M, N, stream);
