@@ -90,13 +90,17 @@ __device__ __forceinline__ float row16_sum(float v)
 }
 
 // G = d / 8 lanes per head; CPL = chunks per lane; NT: non-temporal output stores.
-template <int G, int CPL, bool NT>
+template <int G, int CPL, bool NT, int WPR>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
 {
     const int lane = threadIdx.x & (kLanes - 1);
-    // the token as a uniform value: its row bases live in scalar registers
-    const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    // the token as a uniform value: its row bases live in scalar registers. WPR
+    // waves share a token, part w holding chunks [w * 64 CPL, (w + 1) * 64 CPL):
+    // whole heads, since 64 is a multiple of G (heads are independent).
+    const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int64_t t = unit / WPR;
     if (t >= p.T) return;
+    const int base = (int)(unit - t * WPR) * kLanes * CPL;   // first chunk of this wave
     const int nch = (int)(p.H * G);                  // chunks per token
     const int j = lane % G;                           // chunk index inside the head
     const int i0 = 8 * j;                             // first element of this lane's chunks
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     uint4 v[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c)
-        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((lane + kLanes * c) * 16), 0,
+        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((base + lane + kLanes * c) * 16), 0,
                                                                               kBufferLoadOnce));
 
     // The weight and the token's cos/sin values, likewise by buffer loads issued
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
     uint16_t* orow = p.out + t * p.ldo;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int q = lane + kLanes * c;
+        const int q = base + lane + kLanes * c;
         const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
         float x[8];
 #pragma unroll
@@ -204,13 +208,28 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_qk_prep(QkArgs p)
 template <int G>
 int launch_g(const QkArgs& p, int cpl, hipStream_t stream)
 {
-    const dim3 grid((unsigned)((p.T + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
     const bool nt = p.T * p.H * p.d * 2 >= kNtStoreBytes;
+    const dim3 block(kWavesPerBlock * kLanes);
+    if (cpl >= 4) {
+        // tokens of at least 4 chunks per lane: two waves per token, whole heads each
+        const int64_t nch = p.H * G, per = (nch + 2 * kLanes - 1) / (2 * kLanes);
+        const dim3 g2((unsigned)((2 * p.T + kWavesPerBlock - 1) / kWavesPerBlock));
+#define VDN_CASE2(n)                                                                        \
+        if (per <= n) {                                                                     \
+            if (nt) hipLaunchKernelGGL((k_qk_prep<G, n, true, 2>), g2, block, 0, stream, p);  \
+            else hipLaunchKernelGGL((k_qk_prep<G, n, false, 2>), g2, block, 0, stream, p);    \
+            return check_launch("qk_prep");                                                 \
+        }
+        VDN_CASE2(2) VDN_CASE2(3) VDN_CASE2(4) VDN_CASE2(5) VDN_CASE2(6) VDN_CASE2(8) VDN_CASE2(10)
+        VDN_CASE2(12) VDN_CASE2(16)
+#undef VDN_CASE2
+    }
+    const dim3 grid((unsigned)((p.T + kWavesPerBlock - 1) / kWavesPerBlock));
     switch (cpl) {
-#define VDN_CASE(n)                                                                      \
-    case n:                                                                              \
-        if (nt) hipLaunchKernelGGL((k_qk_prep<G, n, true>), grid, block, 0, stream, p);  \
-        else hipLaunchKernelGGL((k_qk_prep<G, n, false>), grid, block, 0, stream, p);    \
+#define VDN_CASE(n)                                                                         \
+    case n:                                                                                 \
+        if (nt) hipLaunchKernelGGL((k_qk_prep<G, n, true, 1>), grid, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((k_qk_prep<G, n, false, 1>), grid, block, 0, stream, p);    \
         break;
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
         VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
