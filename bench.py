@@ -93,12 +93,29 @@ def _under_load(fn, seconds=2.0):
             "socket_w": round(sum(pw) / len(pw)) if pw else None, "samples": len(clk)}
 
 
+WARM_MS = 60.0
+
+
+def _warm(*fns, ms=WARM_MS):
+    """Runs the given calls for at least `ms` of wall time before a timed region: the
+    part lowers its clock while the host prepares inputs, and needs some tens of
+    milliseconds of load to raise it again (a 1.2 ms GEMM timed right after such a
+    pause reads ~15% slow over its first dozen launches)."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            for f in fns:
+                f()
+        torch.cuda.synchronize()
+
+
 def _time_pair(fa, fb, reps):
     """Mean ms of fa() and of fb(), launched alternately (a, b, a, b, ...) so that a clock
-    that drifts while the part heats up weighs on both alike."""
+    that drifts while the part heats up weighs on both alike (after a warm-up)."""
     import torch
-    fa(), fb()
-    torch.cuda.synchronize()
+    _warm(fa, fb)
     ev = _events(4 * reps)
     for i in range(reps):
         ev[4 * i].record()
@@ -113,11 +130,10 @@ def _time_pair(fa, fb, reps):
 
 
 def _time_region(fn, reps):
-    """Mean ms of fn() over reps launches, from HIP events on the current stream (after one
-    untimed call)."""
+    """Mean ms of fn() over reps launches, from HIP events on the current stream (after a
+    warm-up of untimed calls)."""
     import torch
-    fn()
-    torch.cuda.synchronize()
+    _warm(fn)
     ev = _events(2 * reps)
     for i in range(reps):
         ev[2 * i].record()
@@ -174,7 +190,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     args = ap.parse_args()
