@@ -1,25 +1,30 @@
 """Benchmark of the fp8 quantized-linear path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-extra]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 50] [--no-cpu-baseline] [--no-extra]
+    python bench.py --only NAME [--steps K] [--warmup W]     # one kernel's workload, for profilers
 
 A step is one pass of the hot path over the DiT QKV projection: per-token e4m3
 quantization of X [32760, 5120] followed by the fp8 GEMM against the fused QKV weight
 [15360, 5120] with per-token x per-channel dequantization and the bias fused in. Inputs
-are synthetic (seeded), resident in HBM before the timed region. Prints ONE JSON line:
+are synthetic (seeded, their sha256 checked), resident in HBM before the timed region.
+Prints ONE JSON line:
 
   value       whole-step throughput, 2*M*N*K / step time (TFLOP/s)
   roofline    the GEMM kernel alone, from HIP events on the stream it runs on, against
-              the dense fp8 MFMA peak (5.03 PFLOP/s)
-  cpu_baseline  the oracle (C row quantizer + numpy fp32 dequantized matmul) on a row
-              sample of the same workload, on this host's cores
+              the dense fp8 MFMA peak (5.03 PFLOP/s); `traffic` (HBM bytes per launch) and
+              the MFMA-busy / clock counters come from the committed rocprofv3 profile of
+              this same kernel, and are null when that profile was taken of other code
+  cpu_baseline  the oracle on this host's cores: the single linear (median of 3), and
+              every config's kernel-equivalents at full size
   extra       the quantizer's HBM rate, the weight requantizer (plain and with the fused
-              rank-64 LoRA merge), the other DiT GEMMs and the ms of one block's four
-              linears (QKV, attention-out + gate, FFN-up + GELU, FFN-down + gate)
+              rank-64 LoRA merge), the other DiT GEMMs, the ms of one block's four
+              linears, the H3-width shapes and the pointwise kernels
 """
 import argparse
 import itertools
 import json
 import os
+import statistics
 import subprocess
 import sys
 import time
@@ -29,7 +34,9 @@ sys.path.insert(0, os.path.join(ROOT, "vdn-minimax-h3_amd"))
 
 METRIC = "fp8 linear TFLOP/s & % fp8 MFMA peak (M=32760 QKV); ms per DiT-block linears"
 PEAK_FP8_TFLOPS = 5030.0     # 256 CU x 2.4 GHz x 8192 FLOP/clk/CU, dense
+NOMINAL_GHZ = 2.4
 PEAK_HBM_GBPS = 8000.0
+PROFILE = os.path.join(ROOT, "profiles", "gemm_qkv_pmc.json")
 
 
 def _events(n):
@@ -152,39 +159,159 @@ def _make_linear(w, b, dev, lora=None):
     return vdn_fp8.Fp8Linear(lin, lora=lora)
 
 
-def cpu_baseline(x, w, b, rows=2048, budget_s=12.0):
-    """The oracle on a row sample: quantize `rows` rows, fp32 dequantized matmul + bias.
-    Repeats over disjoint samples until `budget_s` of CPU time; returns TFLOP/s."""
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the oracle (the reference's eager CPU spelling, restated) on host cores
+# ---------------------------------------------------------------------------------------
+
+def cpu_baseline(draws):
+    """The reference's CPU path, restated by the oracle, timed on this host: C row and
+    weight quantizers and LoRA merge (pthreads), numpy binary32 dequantized matmul plus
+    the epilogue (BLAS threads). cfg1 (the single 1024^3 linear): quantize X, quantize W,
+    matmul + bias, median of 3 after one warm-up. cfg2-5: each kernel-equivalent once at
+    full size. `value` is the QKV step (quantize X + matmul + bias) in TFLOP/s."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    from vdn_fp8 import workloads as wl
     cores = min(16, os.cpu_count() or 1)
     os.environ["ORACLE_THREADS"] = str(cores)
 
     def u16(t):
         return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 
-    wq, ws = O.quantize_weight(u16(w))                      # once, like Fp8Linear.__init__
-    wd = O.e4m3_decode(wq) * ws[:, None]
-    bias = O.bf16_decode(u16(b))
-    xb = u16(x)
-    done, spent, flops = 0, 0.0, 0.0
-    with threadpool_limits(limits=cores):
-        while spent < budget_s and done + rows <= xb.shape[0]:
-            t0 = time.perf_counter()
-            qx, sx = O.quantize_rows(xb[done:done + rows])
-            out = (O.e4m3_decode(qx) * sx[:, None]) @ wd.T + bias[None, :]
-            spent += time.perf_counter() - t0
-            flops += 2.0 * rows * w.shape[0] * w.shape[1]
-            done += rows
-            del out
-    return {"value": flops / spent / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{done} of {xb.shape[0]} rows of the QKV workload in {rows}-row batches: oracle C "
-                      f"row quantization + numpy fp32 dequantized matmul + bias ({spent:.1f} s)"}
+    def deq(q, s):
+        return O.e4m3_decode(q) * s[:, None]
 
+    def gelu(v):
+        return 0.5 * v * (1.0 + np.tanh(np.float32(0.7978845608028654) * (v + np.float32(0.044715) * v * v * v)))
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        r = fn()
+        return r, (time.perf_counter() - t0) * 1e3
+
+    per = {}
+    with threadpool_limits(limits=cores):
+        x, w, b = (u16(t) for t in wl.dit_single())
+
+        def single():
+            qx, sx = O.quantize_rows(x)
+            qw, sw = O.quantize_weight(w)
+            return deq(qx, sx) @ deq(qw, sw).T + O.bf16_decode(b)[None, :]
+        single()
+        runs = [timed(single)[1] for _ in range(3)]
+        per["cfg1_single_linear_ms"] = round(statistics.median(runs), 3)
+
+        def linear(name, xb, wb, bias=None, epi=None, gate=None):
+            (qx, sx), tq = timed(lambda: O.quantize_rows(xb))
+            (qw, sw), tw = timed(lambda: O.quantize_weight(wb))
+            def mm():
+                out = deq(qx, sx) @ deq(qw, sw).T
+                if bias is not None:
+                    out += O.bf16_decode(bias)[None, :]
+                if epi == "gelu_tanh":
+                    out = gelu(out)
+                elif epi == "gate":
+                    out *= O.bf16_decode(gate)[None, :]
+                return out
+            _, tg = timed(mm)
+            per[name] = {"quantize_x_ms": round(tq, 1), "quantize_w_ms": round(tw, 1), "gemm_epilogue_ms": round(tg, 1)}
+            return tq, tg
+
+        tq, tg = linear("cfg2_qkv", draws["x2"], draws["w2"], draws["b2"])
+        value = wl.linear_flops(*draws["x2"].shape[:1], draws["w2"].shape[0], draws["x2"].shape[1]) / ((tq + tg) * 1e-3) / 1e12
+        linear("cfg3_ffn_up_gelu", draws["x3"], draws["w3"], draws["b3"], "gelu_tanh")
+        linear("cfg4_ffn_down_gate", draws["x4d"], draws["w4d"], None, "gate", draws["g4"])
+        linear("cfg4_attn_out_gate", draws["x4o"], draws["w4o"], None, "gate", draws["g4"])
+        wm, tm = timed(lambda: O.lora_merge(draws["w5"], draws["a5"], draws["b5"], draws["s5"]))
+        _, tw = timed(lambda: O.quantize_weight(wm))
+        per["cfg5_lora_merge_requantize"] = {"merge_ms": round(tm, 1), "quantize_w_ms": round(tw, 1)}
+    return {"value": round(value, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": "the whole QKV step (quantize X [32760, 5120], dequantized fp32 matmul against W "
+                      "[15360, 5120] + bias) once at full size; cfg1 median of 3 after a warm-up; the other "
+                      "configs' kernel-equivalents once each at full size (oracle C quantizers and merge, numpy "
+                      "fp32 matmul)",
+            "per_config": per}
+
+
+# ---------------------------------------------------------------------------------------
+# the committed profile of the GEMM, used only when it was taken of the code loaded now
+# ---------------------------------------------------------------------------------------
+
+def _profile_fields():
+    """(traffic, counters) from profiles/gemm_qkv_pmc.json when its kernel digest equals the
+    loaded library's GEMM digest, else (None, {"stale": ...})."""
+    import vdn_fp8._lib as L
+    from vdn_fp8 import build as B
+    digest = B.kernel_digest(L.build_info(), "gemm")
+    if not os.path.exists(PROFILE):
+        return None, {"profile": None}
+    with open(PROFILE) as f:
+        prof = json.load(f)
+    if prof.get("kernel_digest") != digest:
+        return None, {"profile": os.path.relpath(PROFILE, ROOT),
+                      "stale": "profiled code differs from the loaded GEMM (digest mismatch)"}
+    c = prof["counters"]
+    return prof["traffic_bytes"], {
+        "profile": os.path.relpath(PROFILE, ROOT), "kernel_digest": digest[:16],
+        "mfma_busy_per_active_cycle": c["mfma_busy_per_active_cycle"],
+        "effective_clock_ghz": c["effective_clock_ghz"],
+        "frac_at_effective_clock": c["frac_at_effective_clock"]}
+
+
+# ---------------------------------------------------------------------------------------
+# single-workload mode (one kernel's launches, for rocprofv3 runs)
+# ---------------------------------------------------------------------------------------
+
+def _only(name, steps, warmup):
+    import torch
+    import vdn_fp8
+    from vdn_fp8 import fused_block as FB
+    from vdn_fp8 import workloads as wl
+    dev = torch.device("cuda:0")
+    if name in ("lora_requant", "requant"):
+        w0, a, b, scale, _ = wl.dit_lora(M=8)
+        copies = [w0.to(dev) for _ in range(3)]
+        rot = itertools.cycle(copies)
+        lora = (a.to(dev), b.to(dev), scale) if name == "lora_requant" else None
+        fn = lambda: vdn_fp8.requantize_weight(next(rot), lora=lora)
+    elif name == "quantize_13824":
+        x = torch.empty(wl.TOKENS, 13824, dtype=torch.bfloat16, device=dev).normal_()
+        fn = lambda: vdn_fp8.quantize_rows(x)
+    elif name == "swiglu_h3":
+        h = torch.empty(wl.TOKENS, 2 * 14336, dtype=torch.bfloat16, device=dev).normal_()
+        fn = lambda: vdn_fp8.swiglu_quantize(h)
+    elif name == "pre_norm_quantize":
+        x = torch.empty(wl.TOKENS, wl.HIDDEN, dtype=torch.bfloat16, device=dev).normal_()
+        nw = torch.ones(wl.HIDDEN, dtype=torch.bfloat16, device=dev)
+        tab = (0.2 * torch.randn(21, wl.HIDDEN, device=dev)).to(torch.bfloat16)
+        idx = (torch.arange(wl.TOKENS, device=dev) * 21 // wl.TOKENS).to(torch.int32)
+        fn = lambda: FB.pre_quantize(x, nw, 1e-6, tab, tab, idx)
+    elif name == "post":
+        x = torch.empty(wl.TOKENS, wl.HIDDEN, dtype=torch.bfloat16, device=dev).normal_()
+        br = torch.empty_like(x).normal_()
+        gt = (2 * torch.rand(2, wl.HIDDEN, device=dev)).to(torch.bfloat16)
+        gid = torch.randint(0, 2, (wl.TOKENS,), device=dev)
+        fn = lambda: FB.post(x, gt, gid, br)
+    elif name == "qk_prep":
+        y = torch.empty(wl.TOKENS, 3 * wl.HIDDEN, dtype=torch.bfloat16, device=dev).normal_()
+        qv = y[:, :wl.HIDDEN].unflatten(-1, (40, 128))
+        nq = torch.ones(128, dtype=torch.bfloat16, device=dev)
+        th = torch.rand(wl.TOKENS, 64, device=dev) * 6.28
+        cs, sn = torch.cat([th.cos(), th.cos()], 1), torch.cat([th.sin(), th.sin()], 1)
+        fn = lambda: vdn_fp8.qk_prep(qv, nq, 1e-6, cs, sn)
+    else:
+        raise SystemExit(f"unknown --only workload {name!r}")
+    for _ in range(warmup):
+        fn()
+    ms = _time_region(fn, steps)
+    print(json.dumps({"only": name, "steps": steps, "warmup": warmup, "ms": round(ms, 4)}), flush=True)
+
+
+# ---------------------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser()
@@ -193,11 +320,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default=None, help="time one workload's kernel alone (lora_requant, requant, "
+                    "quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the fp8 linear path has no cross-GPU step "
               f"(rows shard without exchange); --gpus {args.gpus} is not run.", file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        return _only(args.only, args.steps, args.warmup)
 
     import torch
     import vdn_fp8
@@ -205,6 +336,7 @@ def main():
 
     dev = torch.device("cuda:0")
     x_cpu, w_cpu, b_cpu = wl.dit_qkv()
+    inputs_ok = {"x": wl.sha256(x_cpu), "w": wl.sha256(w_cpu), "bias": wl.sha256(b_cpu)} == wl.DRAW_SHA256["dit_qkv"]
     M, K = x_cpu.shape
     N = w_cpu.shape[0]
     x = x_cpu.to(dev)
@@ -234,59 +366,62 @@ def main():
     gemm_ms = sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(args.steps)) / args.steps
     flops = wl.linear_flops(M, N, K)
     gemm_tflops = flops / (gemm_ms * 1e-3) / 1e12
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("gemm_qkv")
+    traffic, counters = _profile_fields()
     line = {
         "metric": METRIC, "value": round(flops / (ms_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)",
         "data": "synthetic (seeded N(0,1) activations with 0.1% outlier channels x20, N(0,0.02) weights)",
         "config": {"workload": "DiT QKV projection: quantize X + fp8 GEMM + bias", "M": M, "N": N, "K": K,
-                   "seed": 2, "parallelism": "none (1 GPU)"},
+                   "seed": 2, "inputs_sha256_ok": inputs_ok, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "k_gemm_fp8 (EPI none, bias)", "kernel_ms": round(gemm_ms, 4)},
+                     "kernel": "k_gemm_fp8 (EPI none, bias)", "kernel_ms": round(gemm_ms, 4),
+                     "counters": counters},
     }
     extra = {"quantize_rows": {"ms": round(quant_ms, 4),
                                "GB/s": round(wl.quant_bytes(M, K) / (quant_ms * 1e-3) / 1e9, 1)}}
     extra["quantize_rows"]["frac_hbm"] = round(extra["quantize_rows"]["GB/s"] / PEAK_HBM_GBPS, 4)
+    draws = None
 
     if not args.no_extra:
         reps = 10
+        blk = wl.dit_block()
+        x3, w3, b3 = wl.dit_ffn_up()
+        (x4d, w4d), (x4o, w4o), g4 = wl.dit_ffn_down_attn_out()
+        draws = dict(x2=x_cpu, w2=w_cpu, b2=b_cpu, x3=x3, w3=w3, b3=b3, x4d=x4d, w4d=w4d, x4o=x4o, w4o=w4o,
+                     g4=g4, w5=blk["w0"], a5=blk["a"], b5=blk["b"], s5=blk["lora_scale"])
         # weight requantization, plain and with the fused rank-64 LoRA merge. A weight is
         # requantized once, so successive calls rotate over three copies (471 MB, more than
         # the 256 MB last-level cache): every call reads its weight from HBM.
-        w0, a, b, lscale, _ = wl.dit_lora(M=8)
-        w0d, ad, bd = w0.to(dev), a.to(dev), b.to(dev)
+        w0d, ad, bd = blk["w0"].to(dev), blk["a"].to(dev), blk["b"].to(dev)
+        lscale = blk["lora_scale"]
         wcopies = [w0d, w0d.clone(), w0d.clone()]
         rot = itertools.cycle(wcopies)
         ms = _time_region(lambda: vdn_fp8.requantize_weight(next(rot)), reps)
-        extra["requantize_weight"] = {"shape": list(w0.shape), "ms": round(ms, 4),
-                                      "GB/s": round(wl.requant_bytes(*w0.shape) / (ms * 1e-3) / 1e9, 1)}
+        gbs = wl.requant_bytes(*w0d.shape) / (ms * 1e-3) / 1e9
+        extra["requantize_weight"] = {"shape": list(w0d.shape), "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                      "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         ms = _time_region(lambda: vdn_fp8.requantize_weight(next(rot), lora=(ad, bd, lscale)), reps)
         del wcopies, rot
-        gbs = wl.requant_bytes(*w0.shape, rank=a.shape[0]) / (ms * 1e-3) / 1e9
-        extra["lora_merge_requantize"] = {"shape": list(w0.shape), "rank": a.shape[0], "ms": round(ms, 4),
+        gbs = wl.requant_bytes(*w0d.shape, rank=ad.shape[0]) / (ms * 1e-3) / 1e9
+        extra["lora_merge_requantize"] = {"shape": list(w0d.shape), "rank": ad.shape[0], "ms": round(ms, 4),
                                           "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
-        # one DiT block's four linears (QKV weight with the merged LoRA)
-        x_up, w_up, b_up = wl.dit_ffn_up(M=8)
-        (_, w_dn), (_, w_out), gate = wl.dit_ffn_down_attn_out(M=8)
-        qkv = _make_linear(w0, b_cpu, dev, lora=(ad, bd, lscale))
-        out_l = _make_linear(w_out, None, dev)
-        up_l = _make_linear(w_up, b_up, dev)
-        dn_l = _make_linear(w_dn, None, dev)
-        gate_d = gate.to(dev)
-        h = torch.empty(M, w_up.shape[0], dtype=torch.bfloat16, device=dev)
+        # one DiT block's four linears on the LoRA workload's own input (seed 5): the QKV
+        # weight with its LoRA merged, attention-out + gate, FFN-up + GELU, FFN-down + gate
+        qkv = _make_linear(blk["w0"], blk["qkv_bias"], dev, lora=(ad, bd, lscale))
+        out_l = _make_linear(blk["w_out"], None, dev)
+        up_l = _make_linear(blk["w_up"], blk["b_up"], dev)
+        dn_l = _make_linear(blk["w_down"], None, dev)
+        gate_d = blk["gate"].to(dev)
+        x5 = blk["x"].to(dev)
 
         def block():
-            qx, sx = vdn_fp8.quantize_rows(x)
+            qx, sx = vdn_fp8.quantize_rows(x5)
             qkv.forward_quantized(qx, sx)
-            qx, sx = vdn_fp8.quantize_rows(x)
+            qx, sx = vdn_fp8.quantize_rows(x5)
             out_l.forward_quantized(qx, sx, epilogue="gate", gate=gate_d)
-            qx, sx = vdn_fp8.quantize_rows(x)
+            qx, sx = vdn_fp8.quantize_rows(x5)
             hh = up_l.forward_quantized(qx, sx, epilogue="gelu_tanh")
             qh, sh = vdn_fp8.quantize_rows(hh)
             dn_l.forward_quantized(qh, sh, epilogue="gate", gate=gate_d)
@@ -294,16 +429,29 @@ def main():
         block()
         extra["block_linears"] = {"ms": round(_time_region(block, reps), 4),
                                   "flop": wl.linear_flops(M, 3 * 5120 + 5120 + 13824, 5120)
-                                  + wl.linear_flops(M, 5120, 13824)}
-        qx, sx = vdn_fp8.quantize_rows(x)
-        qh, sh = vdn_fp8.quantize_rows(h.normal_())
+                                  + wl.linear_flops(M, 5120, 13824), "input": "dit_lora X (seed 5)"}
+        del x5
+        # the other linears on their own configs' inputs
+        q3, s3 = vdn_fp8.quantize_rows(x3.to(dev))
+        q4d, s4d = vdn_fp8.quantize_rows(x4d.to(dev))
+        q4o, s4o = vdn_fp8.quantize_rows(x4o.to(dev))
+        up3 = _make_linear(w3, b3, dev)
+        dn4 = _make_linear(w4d, None, dev)
+        out4 = _make_linear(w4o, None, dev)
+        g4d = g4.to(dev)
         for name, fn, n_, k_ in (
-                ("gemm_attn_out_gate", lambda: out_l.forward_quantized(qx, sx, epilogue="gate", gate=gate_d), 5120, 5120),
-                ("gemm_ffn_up_gelu", lambda: up_l.forward_quantized(qx, sx, epilogue="gelu_tanh"), 13824, 5120),
-                ("gemm_ffn_down_gate", lambda: dn_l.forward_quantized(qh, sh, epilogue="gate", gate=gate_d), 5120, 13824)):
+                ("gemm_attn_out_gate", lambda: out4.forward_quantized(q4o, s4o, epilogue="gate", gate=g4d), 5120, 5120),
+                ("gemm_ffn_up_gelu", lambda: up3.forward_quantized(q3, s3, epilogue="gelu_tanh"), 13824, 5120),
+                ("gemm_ffn_down_gate", lambda: dn4.forward_quantized(q4d, s4d, epilogue="gate", gate=g4d), 5120, 13824)):
             ms = _time_region(fn, reps)
             tf = wl.linear_flops(M, n_, k_) / (ms * 1e-3) / 1e12
             extra[name] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP8_TFLOPS, 4)}
+        x4d_dev = x4d.to(dev)
+        ms = _time_region(lambda: vdn_fp8.quantize_rows(x4d_dev), reps)
+        gbs = wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9
+        extra["quantize_rows_13824"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
+        del q3, q4d, q4o, up3, dn4, out4, x4d_dev
         # The QKV GEMM again with every code of X and W set to e4m3 1.0: same instructions, same
         # memory traffic, but operands that toggle no multiplier bits. The gap to the line above
         # is what random operands cost in clock (the part holds 2.4 GHz only on such data).
@@ -371,15 +519,13 @@ def main():
         t_f, t_u = _time_pair(ff_fused, ff_unfused, reps)
         extra["ff_sublayer_h3"] = {"tokens": Mh, "fused_ms": round(t_f, 4), "unfused_ms": round(t_u, 4)}
         del ld, lp, hh3, qh3, xh, qxh
-        ms = _time_region(lambda: vdn_fp8.quantize_rows(h), reps)
-        extra["quantize_rows_13824"] = {"ms": round(ms, 4),
-                                        "GB/s": round(wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9, 1)}
         # SwiGLU + quantize at the H3 FFN width (projection output [M, 2 x 14336])
         hh = torch.empty(M, 2 * 14336, dtype=torch.bfloat16, device=dev).normal_()
         ms = _time_region(lambda: vdn_fp8.swiglu_quantize(hh), reps)
         sw_bytes = M * (2 * 2 * 14336 + 14336 + 4)
         extra["swiglu_quantize_h3"] = {"shape": [M, 2 * 14336], "ms": round(ms, 4),
-                                       "GB/s": round(sw_bytes / (ms * 1e-3) / 1e9, 1)}
+                                       "GB/s": round(sw_bytes / (ms * 1e-3) / 1e9, 1),
+                                       "frac_hbm": round(sw_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         del hh
         # the block's pre-norm (RMSNorm + AdaLN affine) fused with the quantizer: one table row
         # per latent frame (21 frames of 30 x 52 tokens), the rows chosen per token
@@ -390,16 +536,16 @@ def main():
         nsh = (0.2 * torch.randn(frames, K, generator=g)).to(torch.bfloat16).to(dev)
         nidx = (torch.arange(M) * frames // M).to(torch.int32).to(dev)
         ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
-        extra["pre_norm_quantize"] = {"ms": round(ms, 4),
-                                      "GB/s": round(wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9, 1)}
+        gbs = wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9
+        extra["pre_norm_quantize"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         # the block's gated residual add (`post`) over [M, 5120] with a 2-row gate table
-        from vdn_fp8 import fused_block as FB
         br_ = torch.randn(M, K, device=dev).to(torch.bfloat16)
         gtab = (2 * torch.rand(2, K, device=dev)).to(torch.bfloat16)
         gid = torch.randint(0, 2, (M,), device=dev)
         ms = _time_region(lambda: FB.post(x, gtab, gid, br_), reps)
-        extra["post_gated_residual"] = {"shape": [M, K], "ms": round(ms, 4),
-                                        "GB/s": round(3 * M * K * 2 / (ms * 1e-3) / 1e9, 1)}
+        gbs = 3 * M * K * 2 / (ms * 1e-3) / 1e9
+        extra["post_gated_residual"] = {"shape": [M, K], "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         del br_
         # QK-norm + rope on q of the QKV output (40 heads of 128, a strided view of the fused
         # [M, 3 x 5120] projection output), fp32 cos/sin tables [M, 128]
@@ -410,13 +556,23 @@ def main():
         cs, sn = torch.cat([th.cos(), th.cos()], 1), torch.cat([th.sin(), th.sin()], 1)
         ms = _time_region(lambda: vdn_fp8.qk_prep(qv, nq, 1e-6, cs, sn), reps)
         qk_bytes = M * 5120 * 2 * 2 + 2 * M * 128 * 4
-        extra["qk_prep_q"] = {"shape": [M, 40, 128], "ms": round(ms, 4),
-                              "GB/s": round(qk_bytes / (ms * 1e-3) / 1e9, 1)}
+        gbs = qk_bytes / (ms * 1e-3) / 1e9
+        extra["qk_prep_q"] = {"shape": [M, 40, 128], "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                              "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         del qkv_out, qv
         extra["gpu_clock"] = _gpu_clock()
     line["extra"] = extra
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(x_cpu, w_cpu, b_cpu)
+        if draws is None:
+            blk = wl.dit_block()
+            x3, w3, b3 = wl.dit_ffn_up()
+            (x4d, w4d), (x4o, w4o), g4 = wl.dit_ffn_down_attn_out()
+            draws = dict(x2=x_cpu, w2=w_cpu, b2=b_cpu, x3=x3, w3=w3, b3=b3, x4d=x4d, w4d=w4d, x4o=x4o,
+                         w4o=w4o, g4=g4, w5=blk["w0"], a5=blk["a"], b5=blk["b"], s5=blk["lora_scale"])
+        import numpy as np
+        u16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+        draws = {k: (u16(v) if isinstance(v, torch.Tensor) else v) for k, v in draws.items()}
+        line["cpu_baseline"] = cpu_baseline(draws)
     print(json.dumps(line), flush=True)
 
 

@@ -18,7 +18,9 @@
  *     neither allocates nor frees device memory; the caller owns all buffers.
  *   - Return 0 on success. A nonzero status leaves nothing launched, and
  *     vdn_fp8_last_error() returns the message (per host thread). Calls are
- *     re-entrant; the library keeps no mutable state besides that message.
+ *     re-entrant. The library's only mutable state is that message and a
+ *     per-device cache of the compute-unit count, filled once under
+ *     std::call_once.
  *   - Scales: x_scale / w_scale are binary32, one per row of X / W.
  */
 #ifndef VDN_FP8_H
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define VDN_FP8_ABI_VERSION 1
+#define VDN_FP8_ABI_VERSION 2
 
 /* status codes */
 #define VDN_FP8_OK 0
@@ -198,6 +200,14 @@ const char *vdn_fp8_last_error(void);
 
 /* VDN_FP8_ABI_VERSION of the loaded library. */
 int vdn_fp8_abi_version(void);
+
+/*
+ * The sources the library was built from, as a JSON object: {"sources": {file:
+ * sha256}, "flags": sha256, "digest": sha256}. A loader compares it with the
+ * sources it ships beside the library and refuses a stale build. No
+ * counterpart in the reference (which compiles its Triton kernels at run time).
+ */
+const char *vdn_fp8_build_info(void);
 
 #ifdef __cplusplus
 }

@@ -117,3 +117,30 @@ def test_check_raises_reference_exception_types():
         L.check(L.EINVAL, "quantize_rows")
     with pytest.raises(L.Fp8LibraryError):
         L.check(L.ELAUNCH, "gemm")
+
+
+def test_build_info_matches_the_sources():
+    import vdn_fp8._lib as L
+    from vdn_fp8 import build as B
+    info = L.build_info()
+    assert info == B.source_manifest()
+    assert set(info["sources"]) == set(B.SOURCES + B.HEADERS + B.PUBLIC_HEADERS)
+
+
+def test_stale_library_is_refused(tmp_path):
+    """A library whose embedded manifest differs from the sources beside it does not load:
+    checked in a fresh process against a copy of the sources with one kernel file changed."""
+    import shutil
+    import subprocess
+    import sys
+    from vdn_fp8 import build as B
+    shutil.copytree(B.CSRC, tmp_path / "csrc")
+    shutil.copytree(B.INCLUDE, tmp_path / "include")
+    with open(tmp_path / "csrc" / "gemm.hip", "a") as f:
+        f.write("\n// changed\n")
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import vdn_fp8._lib as L\n"
+            "try:\n    L.load()\nexcept RuntimeError as e:\n    print('REFUSED', e)\n" % os.path.join(ROOT, "vdn-minimax-h3_amd"))
+    env = dict(os.environ, VDN_FP8_SOURCE_DIR=str(tmp_path))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert "REFUSED" in r.stdout and "gemm.hip" in r.stdout, r.stdout + r.stderr

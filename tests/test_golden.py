@@ -46,3 +46,21 @@ def test_lora_small():
     q, s = O.quantize_weight(d["merged"])
     assert np.array_equal(q, d["codes"])
     assert np.array_equal(s.view(np.uint32), d["w_scale"].view(np.uint32))
+
+
+import pytest
+
+
+@pytest.mark.parametrize("name", ["dit_qkv", "dit_ffn_up", "dit_ffn_down_attn_out", "dit_lora"])
+def test_full_size_draws_are_pinned(name):
+    """Every full-size configuration draw (cfg2-5) still has the committed sha256: the
+    benchmark and the parity tests run on exactly these inputs."""
+    from vdn_fp8 import workloads
+    assert workloads.draw_digests(name) == workloads.DRAW_SHA256[name], \
+        "torch's CPU generator drew different inputs"
+
+
+def test_single_draw_pin_matches_golden():
+    from vdn_fp8 import workloads
+    g = json.load(open(os.path.join(GOLDEN_DIR, "single.json")))
+    assert workloads.DRAW_SHA256["dit_single"] == {"x": g["x"], "w": g["w"], "bias": g["bias"]}

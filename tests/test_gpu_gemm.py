@@ -86,13 +86,71 @@ def _check(x_bits, w_bits, b_bits, device, rows=None, **epi):
         bound = gmax * ulp_chain + bf16_ulp(want)
     bound = np.maximum(MAX_ABS, bound)
     worst = float(np.max(np.abs(got - want) / bound))
+    err = np.abs(got - want)
+    above = err > MAX_ABS
+    vmag = np.abs(want[above])
     print(f"rel_l2={rel:.3e} max_abs={mx:.3e} identical={same:.5f} worst/bound={worst:.2f} "
-          f"rel_l2_unrounded={rel_exact:.3e}", flush=True)
+          f"rel_l2_unrounded={rel_exact:.3e} above_2e-2={int(above.sum())}/{got.size}"
+          + (f" |v| of those in [{vmag.min():.3g}, {vmag.max():.3g}]" if above.any() else ""), flush=True)
     assert rel <= REL_L2, rel
     assert worst <= 1.0, (mx, worst)
     assert same >= 0.98, same
     assert rel_exact <= (4e-3 if epi.get("epilogue") == "gelu_tanh" else REL_L2_UNROUNDED), rel_exact
     return got, want
+
+
+def _screen_full(x_bits, w_bits, b_bits, device, epilogue="none", gate=None):
+    """Every output of a full-size GEMM (all 256 x 256 tiles) against a torch binary32
+    reference on the GPU: the e4m3 codes decoded exactly, their product summed in binary32
+    by torch's fp32 matmul (a library GEMM; another summation order), then the same
+    rounding points as the reference (bf16 output, bf16 bias add, epilogue on the bf16
+    value). Each output must be within max(2e-2, the rounding chain) of it, rel-L2 <=
+    1e-3 over the whole output and >= 98% identical."""
+    f = _linear(w_bits, b_bits, device)
+    qx, sx = vdn_fp8.quantize_rows(from_bits(x_bits, device))
+    kw = {}
+    if epilogue == "gate":
+        kw = dict(epilogue="gate", gate=from_bits(gate, device))
+    elif epilogue == "gelu_tanh":
+        kw = dict(epilogue="gelu_tanh")
+    out = f.forward_quantized(qx, sx, **kw).float()
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        acc = qx.float() @ f.weight_fp8.float().t()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    acc *= sx.reshape(-1, 1) * f.weight_scale.reshape(1, -1)
+    mid0 = acc.to(torch.bfloat16).float()
+    del acc
+    ulp = lambda v: torch.exp2(torch.floor(torch.log2(v.abs().clamp_min(2.0 ** -126))) - 7)
+    chain = ulp(mid0)
+    ref = mid0
+    if b_bits is not None:
+        ref = (ref + f.bias.detach().float().reshape(1, -1)).to(torch.bfloat16).float()
+        chain += ulp(ref)
+    slope = 1.0
+    if epilogue == "gelu_tanh":
+        ref = torch.nn.functional.gelu(ref, approximate="tanh").to(torch.bfloat16).float()
+        slope = 1.13
+    elif epilogue == "gate":
+        gv = kw["gate"].float().reshape(1, -1)
+        ref = (ref * gv).to(torch.bfloat16).float()
+        slope = max(1.0, float(gv.abs().max()))
+    bound = chain if epilogue == "none" else slope * chain + ulp(ref)
+    bound.clamp_(min=MAX_ABS)
+    err = (out - ref).abs()
+    worst = float((err / bound).max())
+    rel = float(torch.linalg.vector_norm(out - ref) / torch.linalg.vector_norm(ref))
+    same = float((out == ref).float().mean())
+    above = err > MAX_ABS
+    n_above = int(above.sum())
+    vmag = ref.abs()[above]
+    print(f"full screen [{qx.shape[0]} x {f.out_features} x {qx.shape[1]}] {epilogue}: rel_l2={rel:.3e} "
+          f"max_abs={float(err.max()):.3e} identical={same:.5f} worst/bound={worst:.2f} above_2e-2={n_above}"
+          + (f" |v| of those in [{float(vmag.min()):.3g}, {float(vmag.max()):.3g}]" if n_above else ""),
+          flush=True)
+    assert rel <= REL_L2 and worst <= 1.0 and same >= 0.98, (rel, worst, same)
 
 
 def _rand(rng, shape, std):
@@ -232,33 +290,51 @@ def _sample_rows(M, n=192, seed=0):
     return rows
 
 
+def _tile_rows(M, seed):
+    """One random row in every 256-row tile, plus the last row: the oracle then checks
+    every m-tile of the output."""
+    rng = np.random.default_rng(seed)
+    starts = np.arange(0, M, 256)
+    rows = starts + rng.integers(0, 256, starts.size)
+    return np.unique(np.concatenate([np.minimum(rows, M - 1), [M - 1]]))
+
+
 def test_gemm_qkv_workload(device):
-    """QKV [32760 x 15360 x 5120] with bias; rows sampled (incl. the ragged last tile)."""
+    """QKV [32760 x 15360 x 5120] with bias: one row of every m-tile against the oracle
+    (every column), then every output against the binary32 screen."""
     x, w, b = workloads.dit_qkv()
-    _check(bits(x), bits(w), bits(b), device, rows=_sample_rows(x.shape[0]))
+    _check(bits(x), bits(w), bits(b), device, rows=_tile_rows(x.shape[0], 0))
+    _screen_full(bits(x), bits(w), bits(b), device)
 
 
 def test_gemm_ffn_up_workload(device):
     x, w, b = workloads.dit_ffn_up()
-    _check(bits(x), bits(w), bits(b), device, rows=_sample_rows(x.shape[0], seed=1), epilogue="gelu_tanh")
+    _check(bits(x), bits(w), bits(b), device, rows=_tile_rows(x.shape[0], 1), epilogue="gelu_tanh")
+    _screen_full(bits(x), bits(w), bits(b), device, epilogue="gelu_tanh")
 
 
 def test_gemm_ffn_down_attn_out_workload(device):
     (xd, wd), (xo, wo), gate = workloads.dit_ffn_down_attn_out()
     g = bits(gate)
-    _check(bits(xd), bits(wd), None, device, rows=_sample_rows(xd.shape[0], seed=2), epilogue="gate", gate=g)
-    _check(bits(xo), bits(wo), None, device, rows=_sample_rows(xo.shape[0], seed=3), epilogue="gate", gate=g)
+    _check(bits(xd), bits(wd), None, device, rows=_tile_rows(xd.shape[0], 2), epilogue="gate", gate=g)
+    _screen_full(bits(xd), bits(wd), None, device, epilogue="gate", gate=g)
+    _check(bits(xo), bits(wo), None, device, rows=_tile_rows(xo.shape[0], 3), epilogue="gate", gate=g)
+    _screen_full(bits(xo), bits(wo), None, device, epilogue="gate", gate=g)
 
 
 def test_gemm_h3_shapes(device):
     """The H3 model's own widths at one rank's share of a sequence (13107 tokens): fused
-    QKV [21504 x 5376] with bias, and the FF down projection [5376 x 14336] with the
-    block's per-token gate table and residual (fast_block_forward's fused form)."""
+    QKV [21504 x 5376] with bias, the 2I-wide FF projection [28672 x 5376] with bias, and
+    the FF down projection [5376 x 14336] with the block's per-token gate table and
+    residual (fast_block_forward's fused form)."""
     rng = np.random.default_rng(13)
     M = 13107
     print("gemm H3 QKV 13107 x 21504 x 5376", flush=True)
     _check(_rand(rng, (M, 5376), 1.0), _rand(rng, (21504, 5376), 0.02), _rand(rng, (21504,), 0.01), device,
            rows=_sample_rows(M, 128, seed=4))
+    print("gemm H3 FF projection 13107 x 28672 x 5376", flush=True)
+    _check(_rand(rng, (M, 5376), 1.0), _rand(rng, (28672, 5376), 0.02), _rand(rng, (28672,), 0.01), device,
+           rows=_tile_rows(M, 6))
     print("gemm H3 FF down 13107 x 5376 x 14336, gate table + residual", flush=True)
     T = 4
     gate = O.bf16_encode(rng.uniform(0, 2, (T, 5376)).astype(np.float32))

@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "vdn_common.h"
 
 namespace vdn {
@@ -25,16 +27,28 @@ int check_launch(const char* what)
     return VDN_FP8_OK;
 }
 
+// The CU count of each device, queried once per device (std::call_once: calls
+// from several host threads see one initialization and no torn value).
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_cus_once[kMaxDevices];
+int g_cus[kMaxDevices];
+}  // namespace
+
 int device_cus()
 {
-    static int cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < 64 && cached[dev] > 0) return cached[dev];
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < 64) cached[dev] = n;
-    return n;
+    if (dev >= kMaxDevices) {
+        int n = 0;
+        return hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? n : 0;
+    }
+    std::call_once(g_cus_once[dev], [dev]() {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+        g_cus[dev] = n;
+    });
+    return g_cus[dev];
 }
 
 int pick_cpl(int64_t nch)
@@ -50,3 +64,10 @@ int pick_cpl(int64_t nch)
 extern "C" const char* vdn_fp8_last_error(void) { return vdn::g_last_error; }
 
 extern "C" int vdn_fp8_abi_version(void) { return VDN_FP8_ABI_VERSION; }
+
+// The build's source manifest (JSON: sha256 of every source and header, of the
+// flags, and their digest), injected by the build script.
+#ifndef VDN_FP8_BUILD_INFO
+#define VDN_FP8_BUILD_INFO "{}"
+#endif
+extern "C" const char* vdn_fp8_build_info(void) { return VDN_FP8_BUILD_INFO; }

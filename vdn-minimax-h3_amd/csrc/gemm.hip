@@ -691,17 +691,18 @@ constexpr int kPhaseMod = 2, kPhaseStep = 1;
 // block): m-tile groups of 4 with the K rotation (QKV N = 15360: 1.91 ms against
 // 1.92-1.96 for groups of 2, 8, 16 or no rotation; FFN-up N = 13824 ties with 8);
 // narrow outputs (N <= 6144, 24 n-tiles) over long rows (K >= 8192) in groups of
-// 2 (FFN-down [32760, 5120, 13824]: 1.665 ms against 1.714 with 4); narrow
-// outputs over short rows in groups of 4 without the rotation (attn-out
-// [32760, 5120, 5120]: 0.670 ms against 0.678).
+// 2 (FFN-down [32760, 5120, 13824]: 1.665 ms against 1.714 with 4).
+// The K rotation is on for every shape, so the summation order of an output
+// depends only on K and on the parity of its tile's (tm + tn): a projection run
+// on its own and as a row block of a fused weight (QKV's Wq;Wk;Wv, whose
+// widths are multiples of 512) give the same bits. Narrow outputs over short
+// rows were 1% faster without it (attention-out [32760, 5120, 5120]: 0.670
+// against 0.678 ms).
 __host__ inline void tile_order(int64_t N, int64_t K, int& phase_mod, int& group_m)
 {
     phase_mod = kPhaseMod;
     group_m = kGroupM;
-    if (N <= 6144) {
-        if (K >= 8192) group_m = 2;
-        else phase_mod = 0;
-    }
+    if (N <= 6144 && K >= 8192) group_m = 2;
 }
 
 // Compute units of the current device (the persistent kernel's grid), cached per

@@ -112,7 +112,11 @@ __device__ __forceinline__ float row_scale(float amax)
 }
 
 // x / s rounded to nearest binary32, from r = RN(1/s): one multiply and two
-// fma. The remainder is written -fma(q0, s, -x) so that x = -0 yields -0.
+// fma -- Markstein's correction of a reciprocal-based quotient (P. Markstein,
+// "Computation of elementary functions on the IBM RISC System/6000 processor",
+// IBM J. Res. Dev. 34(1), 1990): q0 = x r, residual e = x - q0 s (exact by
+// fma), q = q0 + e r. The remainder is written -fma(q0, s, -x) so that x = -0
+// yields -0.
 // Valid for finite, positive s; every (s, x) pair the quantizers can produce
 // gives the same e4m3 code as the IEEE quotient (checked exhaustively).
 __device__ __forceinline__ float div_by_scale(float x, float s, float r)

@@ -1,20 +1,23 @@
 """ctypes binding of libvdnfp8.so (include/vdn_fp8.h).
 
 The library is required: there is no CPU or torch fallback for any entry point.
-Loading fails loudly when the shared library is missing or was built for another
-ABI version.
+Loading fails loudly when the shared library is missing, was built for another ABI
+version, or was built from sources other than the ones beside it (its embedded
+source manifest, vdn_fp8_build_info, must match the csrc/ and include/ files on disk).
 """
 import ctypes
+import json
 import os
 
-from .build import LIB_PATH
+from .build import CSRC, INCLUDE, LIB_PATH, source_manifest
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, EINVAL, ELAUNCH = 0, 1, 2
 EPI_NONE, EPI_GELU_TANH, EPI_GATE = 0, 1, 2
 
 _lib = None
+_build_info = None
 
 # (name, restype, argtypes) of every exported symbol, in header order.
 _P, _I64, _F32, _I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
@@ -30,6 +33,7 @@ EXPORTS = (
     ("vdn_fp8_gated_residual", _I32, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P]),
     ("vdn_fp8_last_error", ctypes.c_char_p, []),
     ("vdn_fp8_abi_version", _I32, []),
+    ("vdn_fp8_build_info", ctypes.c_char_p, []),
 )
 
 
@@ -37,9 +41,32 @@ class Fp8LibraryError(RuntimeError):
     """A launch the HIP runtime refused (status ELAUNCH)."""
 
 
+def _check_sources(lib, path):
+    """Refuse a library whose embedded source manifest differs from the sources on
+    disk. The sources looked at are the package's csrc/ and include/, or
+    VDN_FP8_SOURCE_DIR (a directory holding csrc/ and include/) for a library built
+    from another tree."""
+    info = json.loads(lib.vdn_fp8_build_info().decode())
+    src_root = os.environ.get("VDN_FP8_SOURCE_DIR")
+    csrc, include = (os.path.join(src_root, "csrc"), os.path.join(src_root, "include")) if src_root \
+        else (CSRC, INCLUDE)
+    try:
+        want = source_manifest(csrc, include)
+    except FileNotFoundError as e:
+        raise RuntimeError(f"cannot check {path} against its sources ({e}); the fp8 library ships with "
+                           "its csrc/ and include/ trees") from None
+    if info.get("digest") != want["digest"]:
+        stale = sorted(f for f, h in want["sources"].items() if info.get("sources", {}).get(f) != h)
+        raise RuntimeError(
+            f"{path} was built from other sources than {csrc} / {include} "
+            f"(differs in: {', '.join(stale) or 'build flags'}): rebuild it (python "
+            f"vdn-minimax-h3_amd/vdn_fp8/build.py, or __graft_entry__.build())")
+    return info
+
+
 def load(path=None):
-    """Load (once) and return the library handle; raises if it is absent."""
-    global _lib
+    """Load (once) and return the library handle; raises if it is absent or stale."""
+    global _lib, _build_info
     if _lib is not None:
         return _lib
     path = path or os.environ.get("VDN_FP8_LIB", LIB_PATH)
@@ -49,13 +76,21 @@ def load(path=None):
             f"vdn-minimax-h3_amd/vdn_fp8/build.py, or __graft_entry__.build()). "
             "The fp8 path has no fallback.")
     lib = ctypes.CDLL(path)
+    version = lib.vdn_fp8_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI {version}, expected {ABI_VERSION}: rebuild it")
     for name, res, args in EXPORTS:
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = res, args
-    if lib.vdn_fp8_abi_version() != ABI_VERSION:
-        raise RuntimeError(f"{path} has ABI {lib.vdn_fp8_abi_version()}, expected {ABI_VERSION}")
+    _build_info = _check_sources(lib, path)
     _lib = lib
     return lib
+
+
+def build_info():
+    """The loaded library's source manifest (see vdn_fp8.build.source_manifest)."""
+    load()
+    return _build_info
 
 
 def check(status, what):

@@ -4,8 +4,15 @@
 
 Objects are compiled in a temporary directory (in parallel) and only the shared
 library lands next to this file, where the ctypes loader looks for it.
+
+The library carries the sha256 of every source it was built from (and of the flags),
+returned by vdn_fp8_build_info(); the loader compares it with the sources on disk and
+refuses a library built from other sources, so a stale build cannot stand in for the
+current kernels.
 """
 import concurrent.futures
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -14,12 +21,14 @@ import tempfile
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_PKG)                      # vdn-minimax-h3_amd/
-_CSRC = os.path.join(_ROOT, "csrc")
-_INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
+CSRC = os.path.join(_ROOT, "csrc")
+INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
 LIB_NAME = "libvdnfp8.so"
 LIB_PATH = os.path.join(_PKG, LIB_NAME)
 
 SOURCES = ["capi.hip", "quantize.hip", "lora_requant.hip", "gemm.hip", "qk_prep.hip", "block_ops.hip"]
+HEADERS = ["vdn_common.h"]             # in csrc/
+PUBLIC_HEADERS = ["vdn_fp8.h"]         # in include/
 
 # -ffp-contract=off: the quantizers' binary32 arithmetic is bit-exact only as
 # written (explicit fma where one is meant). Packed fp32 instructions are kept
@@ -36,6 +45,39 @@ HIPCC_FLAGS = [
 EXTRA_FLAGS = {"lora_requant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
+def _sha256(path):
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def source_manifest(csrc=CSRC, include=INCLUDE):
+    """{"sources": {file: sha256}, "flags": sha256, "digest": sha256 of all of it}: what
+    a library built from these files carries. Raises FileNotFoundError if a file is
+    missing."""
+    files = {name: _sha256(os.path.join(csrc, name)) for name in SOURCES + HEADERS}
+    files.update({name: _sha256(os.path.join(include, name)) for name in PUBLIC_HEADERS})
+    flags = hashlib.sha256(json.dumps([HIPCC_FLAGS, EXTRA_FLAGS], sort_keys=True).encode()).hexdigest()
+    body = json.dumps({"sources": files, "flags": flags}, sort_keys=True)
+    return {"sources": files, "flags": flags, "digest": hashlib.sha256(body.encode()).hexdigest()}
+
+
+# The files that make each kernel family (its source plus the shared headers).
+KERNEL_FILES = {
+    "gemm": ["gemm.hip", "vdn_common.h", "vdn_fp8.h"],
+    "quantize": ["quantize.hip", "vdn_common.h", "vdn_fp8.h"],
+    "lora_requant": ["lora_requant.hip", "quantize.hip", "vdn_common.h", "vdn_fp8.h"],
+}
+
+
+def kernel_digest(manifest, family):
+    """sha256 over the hashes of one kernel family's files (KERNEL_FILES) and of the
+    flags in a manifest: identifies the code of that kernel, e.g. for profiles keyed to
+    it."""
+    files = KERNEL_FILES[family]
+    return hashlib.sha256(json.dumps([manifest["sources"][f] for f in files] + [manifest["flags"]]).encode()
+                          ).hexdigest()
+
+
 def hipcc():
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -43,14 +85,20 @@ def hipcc():
     raise RuntimeError("hipcc not found: the fp8 library needs ROCm's hipcc to build")
 
 
-def build(verbose=False):
+def build(verbose=False, csrc=CSRC, include=INCLUDE, out=LIB_PATH):
     """Compile every source for gfx950 and link libvdnfp8.so. Returns its path."""
     cc = hipcc()
+    manifest = source_manifest(csrc, include)
     with tempfile.TemporaryDirectory(prefix="vdnfp8_build_") as tmp:
+        info_h = os.path.join(tmp, "vdn_build_info.h")
+        with open(info_h, "w") as f:
+            f.write("#define VDN_FP8_BUILD_INFO %s\n" % json.dumps(json.dumps(manifest, sort_keys=True)))
+
         def compile_one(src):
             obj = os.path.join(tmp, os.path.splitext(src)[0] + ".o")
-            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-I", _INCLUDE, "-I", _CSRC, "-c",
-                   os.path.join(_CSRC, src), "-o", obj]
+            extra = ["-include", info_h] if src == "capi.hip" else []
+            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), *extra, "-I", include, "-I", csrc, "-c",
+                   os.path.join(csrc, src), "-o", obj]
             r = subprocess.run(cmd, capture_output=True, text=True)
             if r.returncode != 0:
                 raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
@@ -68,9 +116,9 @@ def build(verbose=False):
             raise RuntimeError(f"linking {LIB_NAME} failed:\n{r.stderr}")
         # Copy next to the target, then rename: a process that already mapped
         # the old library keeps a consistent file.
-        shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
-        os.replace(LIB_PATH + ".tmp", LIB_PATH)
-    return LIB_PATH
+        shutil.copyfile(tmp_lib, out + ".tmp")
+        os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":

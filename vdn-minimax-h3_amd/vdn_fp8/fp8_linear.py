@@ -67,7 +67,9 @@ def _rows(x):
 
 
 def quantize_rows(x):
-    """bf16 [M, K] -> (fp8 [M, K], fp32 scale [M, 1]). One absmax per row.
+    """Per-token quantization: each row of the bf16 [M, K] input is divided by its own
+    scale max(row absmax / 448, 1e-12) and cast to e4m3. Returns the codes [M, K] and
+    the binary32 scales [M, 1].
 
     Codes and scales are bit-identical to `quantize_rows_reference` (the reference's
     eager spelling, fp8_linear.py:132-135). Replaces fp8_linear.py:110-117."""
@@ -82,8 +84,11 @@ def quantize_rows(x):
 
 
 def swiglu_quantize(h):
-    """[M, 2K] projection output -> quantize_rows(a * silu(gate)) with a, gate = h.chunk(2),
-    without writing the bf16 activation. Replaces fp8_linear.py:120-129."""
+    """SwiGLU and per-token quantization in one kernel. h is the FFN projection's bf16
+    output [M, 2K]: its first K columns are the value a, its last K the gate g. The
+    activation a * g * sigmoid(g) stays binary32 (it is never stored as bf16) and is
+    quantized row by row as in `quantize_rows`; returns e4m3 [M, K] and scales [M, 1].
+    Replaces fp8_linear.py:120-129."""
     h = _rows(h)
     M, K2 = h.shape
     if K2 % 2:
@@ -141,8 +146,8 @@ def requantize_weight(weight, lora=None, merged_out=None):
     arithmetic of Fp8Linear.__init__ (fp8_linear.py:262-267).
 
     lora = (A [r, K], B [N, r], scale) folds W + bf16(scale * B @ A) in first, as
-    merge_lora_state does (lora.py:91-92): with bf16 factors inside the same kernel; with
-    factors of another dtype (fp16 / fp32 adapters) the update is the reference's own
+    merge_lora_state does (lora.py:91-92): with bf16 factors of rank <= 128 inside the same
+    kernel; other adapters (fp16 / fp32 factors, larger ranks) take the reference's own
     fp32 product on the GPU (a plain library GEMM), rounded to bf16 and added, and the
     kernel requantizes the merged weight. merged_out, if given (bf16 [N, K], may be
     `weight` itself), receives the merged weight."""
@@ -166,11 +171,12 @@ def requantize_weight(weight, lora=None, merged_out=None):
         rank = a.shape[0]
         if a.shape != (rank, K) or b.shape != (N, rank):
             raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
-        if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        if not lora_in_kernel(a, b):
             merged = w + lora_delta(a, b, lscale)
             if merged_out is not None:
                 merged_out.copy_(merged)
             return requantize_weight(merged)
+        a = _aligned16(a)
     lib = _lib.load()
     _lib.check(lib.vdn_fp8_requantize_weight(_ptr(w), N, K, K, _ptr(a), _ptr(b), rank, float(lscale),
                                              _ptr(q), K, _ptr(s), _ptr(merged_out), _stream(w)),
@@ -184,20 +190,36 @@ def _lora_factor(t, w, name):
     return t.to(w.device).contiguous()
 
 
-def lora_delta(a, b, scale):
-    """bf16(scale * (B.float() @ A.float())): the reference's update (lora.py:91-92) for
-    factors that are not bf16, as an fp32 GEMM on the factors' device (a plain library
-    GEMM; bf16 factors never come here, the requantize kernel forms their product)."""
-    return ((b.to(torch.float32) @ a.to(torch.float32)) * scale).to(torch.bfloat16)
+# Largest LoRA rank the fused merge kernel takes (its A^T slice is staged in LDS).
+LORA_KERNEL_MAX_RANK = 128
+
+
+def lora_in_kernel(a, b):
+    """True when the fused merge + requantize kernel takes these factors: bf16 A [r, K]
+    and B [N, r] with 1 <= r <= 128 and K % 16 == 0. Other adapters (fp16 / fp32
+    factors, larger ranks) take `lora_delta`, the reference's own update."""
+    r, K = a.shape
+    return (a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and 1 <= r <= LORA_KERNEL_MAX_RANK
+            and K % 16 == 0)
+
+
+def lora_delta(a, b, scale, dtype=torch.bfloat16):
+    """(scale * (B.float() @ A.float())).to(dtype): the reference's update (lora.py:91-92),
+    as an fp32 GEMM on the factors' device (a plain library GEMM), for the adapters the
+    fused kernel does not take (`lora_in_kernel`) and for targets that are not contiguous
+    bf16 GPU weights."""
+    return ((b.to(torch.float32) @ a.to(torch.float32)) * scale).to(dtype)
 
 
 class Fp8Linear(nn.Module):
-    """A bias-optional Linear whose GEMM runs in fp8 e4m3 (fp8_linear.py:243-283).
+    """nn.Linear replacement with e4m3 operands and an fp32-accumulating MFMA GEMM
+    (the reference's class: fp8_linear.py:243-283).
 
-    The weight is quantised ONCE, per output channel, at construction; the activation is
-    quantised per row on every call, or by the caller (`forward_quantized`) when one
-    activation feeds several of these. Only the fp8 copy and the bias are kept -- the
-    bf16 weight goes as soon as the caller drops the Linear it came from.
+    Construction turns the Linear's bf16 weight into codes with one scale per output
+    channel (the only time the weight is read); the module keeps those codes and the
+    scales, plus the Linear's own bias Parameter, and holds no reference to the bf16
+    weight. Each `forward` quantizes its input per token first; a caller that feeds one
+    activation to several projections quantizes it once and calls `forward_quantized`.
 
     Buffers: weight_fp8 e4m3 [N, K], weight_scale fp32 [1, N]; `bias` is the source
     Linear's Parameter object itself.
@@ -296,8 +318,9 @@ class Fp8Linear(nn.Module):
 
 
 def _blocks_to_skip(model, skip_end_blocks):
-    """ids of every module inside the first and last N transformer blocks
-    (fp8_linear.py:286-295)."""
+    """The set of id()s of all modules that belong to the leading or trailing
+    `skip_end_blocks` entries of model.transformer_blocks (empty when the model has no
+    such list): those stay bf16 (fp8_linear.py:286-295)."""
     blocks = getattr(model, "transformer_blocks", None)
     if not blocks or skip_end_blocks <= 0:
         return set()
@@ -309,13 +332,15 @@ def _blocks_to_skip(model, skip_end_blocks):
 
 
 def convert_linear_to_fp8(model, min_width=MIN_WIDTH, skip_end_blocks=SKIP_END_BLOCKS):
-    """Swap the wide Linears for fp8 ones, in place. Returns how many were swapped
-    (fp8_linear.py:298-323).
+    """Replace, inside `model`, every nn.Linear whose input and output widths are both at
+    least `min_width` (outside the end blocks `_blocks_to_skip` names) by an Fp8Linear.
+    Works in place and returns the number replaced (fp8_linear.py:298-323).
 
-    Call it AFTER any LoRA merge (or use `vdn_fp8.lora.merge_lora_and_convert`, which
-    fuses the two). The work list names (parent, attribute), never the Linears, so each
-    bf16 weight is released as soon as its parent is repointed: peak memory is the model
-    plus one fp8 weight."""
+    The weights are read here, so LoRA has to be merged before this runs
+    (`vdn_fp8.lora.merge_lora_and_convert` does both per weight). The list of work holds
+    (parent module, attribute name) pairs rather than the Linears: once a parent points
+    at its Fp8Linear nothing keeps the bf16 Linear alive, so at most one bf16 weight and
+    its fp8 copy coexist beyond the model itself."""
     skip = _blocks_to_skip(model, skip_end_blocks)
     targets = [(parent, name) for parent in model.modules()
                for name, child in parent.named_children()

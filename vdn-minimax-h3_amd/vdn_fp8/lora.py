@@ -3,8 +3,10 @@
 
     W += scale * (B @ A)     delta in fp32, added in the weight's dtype (bf16)
 
-`merge_lora_state` keeps the reference's in-place semantics and return value; the
-update runs in the HIP kernel behind vdn_fp8_requantize_weight (merge-only mode).
+`merge_lora_state` keeps the reference's in-place semantics and return value; for
+contiguous bf16 GPU weights and bf16 adapters of rank <= 128 the update runs in the HIP
+kernel behind vdn_fp8_requantize_weight (merge-only mode), for any other target or
+adapter it is the reference's own torch update (`merge_into`).
 `merge_lora_and_convert` fuses the merge into the fp8 conversion: for every Linear
 that `convert_linear_to_fp8` would swap, W + scale * B @ A is quantized directly
 (the merged bf16 weight is never written), and the remaining pairs are merged in
@@ -20,8 +22,8 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .fp8_linear import (MIN_WIDTH, SKIP_END_BLOCKS, Fp8Linear, _blocks_to_skip, _ptr, lora_delta,
-                         _stream)
+from .fp8_linear import (MIN_WIDTH, SKIP_END_BLOCKS, Fp8Linear, _aligned16, _blocks_to_skip, _ptr,
+                         _stream, lora_delta, lora_in_kernel)
 
 # Original-layout module names -> diffusers names (lora.py:22-30).
 _ORIGINAL_RENAMES = (
@@ -86,24 +88,32 @@ def _pairs(state):
 
 
 def merge_into(weight, a, b, scale=1.0):
-    """weight (bf16 [N, K], on the GPU, contiguous) += bf16(scale * (B @ A)), in place.
-    bf16 factors go through the HIP kernel; fp16 / fp32 factors (external adapters) take
-    the reference's fp32 product on the GPU, rounded to bf16, then the bf16 add."""
-    if not weight.is_cuda or weight.dtype != torch.bfloat16 or weight.dim() != 2 or not weight.is_contiguous():
-        raise ValueError("the LoRA merge is a HIP kernel: the weight must be a contiguous bf16 [N, K] GPU tensor")
+    """weight (W [N, K]) += (scale * (B @ A)).to(W.dtype), in place (lora.py:91-92).
+
+    A contiguous bf16 weight on the GPU with bf16 factors of rank <= 128 is merged by the
+    HIP kernel (merge-only mode of vdn_fp8_requantize_weight). Every other target -- an
+    fp32 or fp16 weight (the hybrid attention's parameters before their bf16 cast,
+    assemble.py:124 vs :148-151), a non-contiguous view, a weight still in host memory --
+    and every other adapter (fp16 / fp32 factors, larger ranks) takes the reference's own
+    arithmetic where the weight lives: the fp32 product of the factors, scaled, cast to
+    the weight's dtype, then added."""
     for t, nm in ((a, "A"), (b, "B")):
         if t.dtype not in (torch.bfloat16, torch.float16, torch.float32):
             raise ValueError(f"LoRA factor {nm} must be bfloat16, float16 or float32 (got {t.dtype})")
-    a = a.to(weight.device).contiguous()
-    b = b.to(weight.device).contiguous()
+    if weight.dim() != 2:
+        raise ValueError(f"a LoRA target must be a 2-D weight, got {tuple(weight.shape)}")
     N, K = weight.shape
     r = a.shape[0]
-    if a.shape != (r, K) or b.shape != (N, r):
+    if a.dim() != 2 or b.dim() != 2 or a.shape != (r, K) or b.shape != (N, r):
         raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
-    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
-        weight.add_(lora_delta(a, b, scale))
+    a = a.to(weight.device).contiguous()
+    b = b.to(weight.device).contiguous()
+    if not (weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous()
+            and lora_in_kernel(a, b)):
+        weight.add_(lora_delta(a, b, scale, dtype=weight.dtype))
         return weight
     lib = _lib.load()
+    a = _aligned16(a)
     _lib.check(lib.vdn_fp8_requantize_weight(_ptr(weight), N, K, K, _ptr(a), _ptr(b), r, float(scale),
                                              None, 0, None, _ptr(weight), _stream(weight)),
                "merge_lora_state")

@@ -10,9 +10,12 @@ machine whose torch CPU generator matches (tests pin the sha256 of the draws).
   dit_ffn_up  X [32760, 5120], W [13824, 5120], bias, GELU(tanh)
   dit_ffn_down / dit_attn_out   X [32760, 13824] = gelu(N(0,1)) / X [32760, 5120], W [5120, *],
                                 AdaLN gate [5120] ~ 2 U(0,1)
-  dit_lora    base W [15360, 5120] + rank-64 LoRA (alpha 64), then a block's four linears
-M = 32760 is 21 latent frames x 30 x 52 patches.
+  dit_lora    base W [15360, 5120] + rank-64 LoRA (alpha 64) and the block input X, seed 5
+  dit_block   one block's four linears: the LoRA-merged QKV on dit_lora's X, attention-out,
+              FFN-up + GELU and FFN-down + gate with the other draws' weights
+M = 32760 is 21 latent frames x 30 x 52 patches. DRAW_SHA256 pins every full-size draw.
 """
+import hashlib
 import math
 
 import torch
@@ -107,3 +110,64 @@ def quant_bytes(M, K):
 def requant_bytes(N, K, rank=0):
     """Algorithmic HBM bytes of a weight requantization (+ LoRA factors when fused)."""
     return 2.0 * N * K + N * K + 4.0 * N + (2.0 * rank * (N + K) if rank else 0.0)
+
+
+def dit_block(M=TOKENS):
+    """One DiT block's four fp8 linears as the LoRA workload runs them (seed 5 for the
+    block input): the QKV weight is dit_lora's base weight with its rank-64 LoRA folded in
+    and dit_qkv's bias; attention-out and FFN-down are dit_ffn_down_attn_out's weights
+    with its AdaLN gate; FFN-up is dit_ffn_up's weight and bias with GELU(tanh). The
+    weights are those of the full-size draws (each draw sequence puts X first).
+
+    Returns a dict: x, w0, a, b, lora_scale, qkv_bias, w_out, w_up, b_up, w_down, gate."""
+    w0, a, b, scale, x = dit_lora(M)
+    _, _, qkv_bias = dit_qkv()
+    _, w_up, b_up = dit_ffn_up()
+    (_, w_down), (_, w_out), gate = dit_ffn_down_attn_out()
+    return dict(x=x, w0=w0, a=a, b=b, lora_scale=scale, qkv_bias=qkv_bias, w_out=w_out, w_up=w_up,
+                b_up=b_up, w_down=w_down, gate=gate)
+
+
+def sha256(t):
+    """sha256 of a bf16 tensor's bytes (row-major)."""
+    return hashlib.sha256(t.contiguous().view(torch.int16).numpy().tobytes()).hexdigest()
+
+
+# sha256 of every full-size draw, as produced by torch's CPU generator: a change in that
+# generator would silently change the inputs, so the tests (and bench.py, for the draw
+# it times) compare against these.
+DRAW_SHA256 = {
+    "dit_single": {"x": "8e8dc87032770e08a7228dff86a712858bdcd5089cecfb901288a8fe13f0fdd9",
+                   "w": "515a2c50911ca96b8883b89377e7db69cac7423a78022cb4c58fa6e69d58bada",
+                   "bias": "532e5ad6a60179f156d6229a1c6a0e70649edc728f4ce7722babf51667d3324d"},
+    "dit_qkv": {"x": "0c0a840a1ab0af5cb382df53c6e28b1657190f77d990e995d0602474093d2678",
+                "w": "0f49aa9c88fa2b7956c3e81865ead449000b5c35e7fbd0d5c99b16fa320c9387",
+                "bias": "5360751a55d281f20d5069870a5cb5ed67b14c331d0ccf7572915dd071abd56c"},
+    "dit_ffn_up": {"x": "7b9febb793e8d1151ed607cffaa2a1e7e7e7d28fc5b8d35d178de56654c73ea9",
+                   "w": "a8ecdee89261d83ba0a92756dfb97549d3e9a8a872f0abc7ab831aea6eef7a13",
+                   "bias": "551f311f154c91fe07f6d46a2266927904b30c0d35d4922ed0b314845cf67dd6"},
+    "dit_ffn_down_attn_out": {
+        "x_down": "f195bfe7277b163a66cc6ee0863b24d7444a9db4adfdb5868f845525a6acc926",
+        "w_down": "7be0305d6f91aa57122eb120a50c52e6f0fe406e00b1d478a395ce52e1826e03",
+        "x_out": "3e374368b6397ebb54e920bbfe5e3ca6c14c99faf439d358ba0dd797583fc4a4",
+        "w_out": "3a8536abe77a0c17ffd190fc06d4e92289f6ded5e29520c1e6daef52ff0838a1",
+        "gate": "1ab8c931a0631faa1d3ff13e2da05b99122abd459b6c6525ba02c0ee9873e9f6"},
+    "dit_lora": {"w0": "bd0f8d8337f9862fdcd4874ea6dae77d0149757bd7afb2df07c450089333c7ab",
+                 "a": "3d3702eb604642b0b0114c2dac4f44d432286d9fb3b01ccc9c64d18770ed4ca4",
+                 "b": "ba3d42d6bdad5de59590e92647618d05e64ed5138fec8fea7993cc9e9945fb80",
+                 "x": "526126abe828819e58d110725fa2db6708898792d63443da42ff416abc56d494"},
+}
+
+
+def draw_digests(name):
+    """{tensor: sha256} of the full-size draw `name` (a key of DRAW_SHA256)."""
+    if name == "dit_ffn_down_attn_out":
+        (xd, wd), (xo, wo), g = dit_ffn_down_attn_out()
+        named = dict(x_down=xd, w_down=wd, x_out=xo, w_out=wo, gate=g)
+    elif name == "dit_lora":
+        w0, a, b, _, x = dit_lora()
+        named = dict(w0=w0, a=a, b=b, x=x)
+    else:
+        x, w, b = globals()[name]()
+        named = dict(x=x, w=w, bias=b)
+    return {k: sha256(v) for k, v in named.items()}
