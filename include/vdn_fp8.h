@@ -22,6 +22,10 @@
  *     per-device cache of the compute-unit count, filled once under
  *     std::call_once.
  *   - Scales: x_scale / w_scale are binary32, one per row of X / W.
+ *   - Table indices (gate_index, mod_index) outside the table are clamped into
+ *     it; the reference's index_select raises on them instead (a deliberate
+ *     difference: the kernels read the index with the row's data and never
+ *     fault or report; check the range on the host if an error is wanted).
  */
 #ifndef VDN_FP8_H
 #define VDN_FP8_H
