@@ -278,8 +278,8 @@ def _only(name, steps, warmup):
         rot = itertools.cycle(copies)
         lora = (a.to(dev), b.to(dev), scale) if name == "lora_requant" else None
         fn = lambda: vdn_fp8.requantize_weight(next(rot), lora=lora)
-    elif name == "quantize_13824":
-        x = torch.empty(wl.TOKENS, 13824, dtype=torch.bfloat16, device=dev).normal_()
+    elif name in ("quantize_13824", "quantize_5120"):
+        x = torch.empty(wl.TOKENS, int(name.split("_")[1]), dtype=torch.bfloat16, device=dev).normal_()
         fn = lambda: vdn_fp8.quantize_rows(x)
     elif name == "swiglu_h3":
         h = torch.empty(wl.TOKENS, 2 * 14336, dtype=torch.bfloat16, device=dev).normal_()
@@ -321,7 +321,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time one workload's kernel alone (lora_requant, requant, "
-                    "quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep)")
+                    "quantize_5120, quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the fp8 linear path has no cross-GPU step "

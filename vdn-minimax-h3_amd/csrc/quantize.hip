@@ -29,6 +29,8 @@ constexpr int kWavesPerBlock = 4;  // waves per workgroup
 constexpr int64_t kNtStoreBytes = 256ll << 20;
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 template <bool NT>
 __device__ __forceinline__ void store_normed(uint4* p, uint4 v)
 {
@@ -277,142 +279,185 @@ __device__ __forceinline__ float wave_sum_f32(float v)
     return v;
 }
 
-// WPR waves per row (1, 2 or 4), the row in VGPRs:
+// The block's pre-norm fused with the per-token quantization:
 //   rstd   = 1 / sqrt(sum_k x^2 / K + eps)                       (binary32)
-//   n[k]   = bf16(((x[k] * rstd) * w[k]) * (1 + scale[i][k]) + shift[i][k])
+//   n[k]   = bf16(fma(x[k] * rstd, f[k], shift[i][k]))   f = w (1 + scale[i]),
+//                                                         (x[k] * rstd) * w[k] without a table
 //   y, s   = the quantize_rows arithmetic on n
-// with i = mod_index[row] (clamped into the table). The affine chain is held in
-// binary32 and rounded once, as the compiled `pre` of fused_block.py does; the
-// codes follow from the bf16 n exactly as quantize_rows' do. Wave part p of a
-// row holds chunks p*64 + lane + 64*WPR*c; the partial sums of squares and the
-// row maxima of the waves of a row meet in LDS (summed in part order, so every
-// wave of the row gets the same rstd). The weight and table chunks are loaded
-// with the row, before the reductions, so their latency hides behind them.
-template <int CPL, int WPR, bool NT>
-__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant(NormArgs p)
+// with i = mod_index[row] (clamped into the table). The affine's association
+// differs from the compiled `pre`'s ((x rstd) w)(1 + scale) + shift (its fp32
+// operation order is unspecified); the normed values stay within one bf16
+// rounding of the float64 restatement. The codes follow from the bf16 n exactly
+// as quantize_rows' do. Without codes (QUANT false) the call is the pre-norm
+// alone, with the same n, so the fused and unfused forms of a block give the
+// same bits.
+// WPR waves share a row (1, 2 or 4): wave part p holds chunks p*64 + lane +
+// 64*WPR*c; the partial sums of squares and the row maxima meet in LDS (summed
+// in part order, so every wave of the row gets the same rstd). Each group of
+// WPR waves walks a contiguous block of `rb` rows, the next row's loads in
+// flight while the current one is computed. The per-column factors f and the
+// shift (binary32) stay in VGPRs and are formed again only when the table row
+// changes (a frame of tokens shares one), so a row costs its own bytes and
+// three binary32 operations per element before the rounding.
+template <int CPL, int WPR, bool NT, bool AFFINE, bool QUANT>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant_blocks(NormArgs p, int64_t rb)
 {
     static_assert(kWavesPerBlock % WPR == 0, "rows per workgroup");
     __shared__ float ssum[kWavesPerBlock];
     __shared__ uint32_t smax[kWavesPerBlock];
-    // (the wave index as a uniform value: the row and its table index then live in
-    // scalar registers, and the index is read by a scalar load)
     const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int part = wave % WPR;
-    const int64_t row = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
-    if (WPR == 1 && row >= p.M) return;
-    const bool valid = row < p.M;                    // (WPR > 1: every wave reaches the barriers)
-    const int64_t rr = valid ? row : 0;
+    const int64_t gid = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
+    const int64_t row0 = gid * rb;
+    const int64_t row_end = min(p.M, row0 + rb);
     const int nch = (int)(p.K >> 3);
-    // Buffer loads: chunks past K (and every chunk of a row past M) fall outside the
-    // descriptor's range and read as zeros, with no branch, so the loads of a row
-    // are in flight together (a conditional plain load here made the compiler wait
-    // for each one before issuing the next).
     const int rowbytes = nch * 16;
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.x + rr * p.ldx), 0, valid ? rowbytes : 0, 0x00020000);
-    uint4 v[CPL];
+    auto chunk_off = [&](int c) { return (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u; };
+    // Rows and row addresses as wave-uniform values (scalar registers): the buffer
+    // descriptors built from them need no per-lane loop.
+    auto uniform = [](int64_t v) -> int64_t {
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+    // Buffer loads: chunks past K (and every chunk of a row past the block) fall
+    // outside the descriptor's range and read as zeros, with no branch.
+    auto load_row = [&](int64_t row, uint4 (&v)[CPL]) {
+        const bool valid = row < row_end;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.x + (valid ? row : 0) * p.ldx)), 0, valid ? rowbytes : 0, 0x00020000);
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const uint32_t off = (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u;
-        v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, kBufferLoadOnce));
-    }
-    // the row's loads are issued before the table index is read (a scalar load the
-    // table addresses wait for), so they do not wait behind it
-    __builtin_amdgcn_sched_barrier(0);
-    int64_t ti = 0;
-    if (p.mod_index) ti = min(max((int64_t)p.mod_index[rr], (int64_t)0), p.mod_rows - 1);
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.weight ? p.weight : p.x), 0, p.weight ? rowbytes : 0, 0x00020000);
-    const __amdgpu_buffer_rsrc_t scs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.mod_scale ? p.mod_scale + ti * p.ldmod : p.x), 0, p.mod_scale ? rowbytes : 0, 0x00020000);
-    const __amdgpu_buffer_rsrc_t shs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.mod_shift ? p.mod_shift + ti * p.ldmod : p.x), 0, p.mod_shift ? rowbytes : 0, 0x00020000);
-    const uint4 one = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // 1.0
-    uint4 wv[CPL], sc[CPL], sh[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const uint32_t off = (uint32_t)(part * kLanes + lane + kLanes * WPR * c) * 16u;
-        wv[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
-        if (!p.weight) wv[c] = one;
-        sc[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(scs, off, 0, 0));
-        sh[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(shs, off, 0, 0));
-    }
-    // sum of squares straight from the packed bf16 pairs (v_dot2c_f32_bf16: no
-    // unpacking), four partial sums to keep the chains short
-    float ssp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            ssp[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4[e]),
-                                                     __builtin_bit_cast(bf16x2_t, w4[e]), ssp[e], false);
-    }
-    float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
-    if (WPR > 1) {
-        if (lane == 0) ssum[wave] = ss;
-        __syncthreads();
-        ss = ssum[(wave / WPR) * WPR];
-#pragma unroll
-        for (int w = 1; w < WPR; ++w) ss += ssum[(wave / WPR) * WPR + w];
-    }
-    const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
-    // Opaque to the optimizer: the second sweep unpacks the bf16 pairs again
-    // instead of keeping the first sweep's binary32 copies live (twice the VGPRs).
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) asm volatile("" : "+v"(v[c].x), "+v"(v[c].y), "+v"(v[c].z), "+v"(v[c].w));
-
-    uint32_t m2 = 0;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-        const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
-        const uint32_t sw[4] = {sc[c].x, sc[c].y, sc[c].z, sc[c].w}, hw[4] = {sh[c].x, sh[c].y, sh[c].z, sh[c].w};
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float a = (bf16_lo(xw[e]) * rstd) * bf16_lo(ww[e]);
-            float b = (bf16_hi(xw[e]) * rstd) * bf16_hi(ww[e]);
-            if (p.mod_scale) {
-                a = a * (1.0f + bf16_lo(sw[e])) + bf16_lo(hw[e]);
-                b = b * (1.0f + bf16_hi(sw[e])) + bf16_hi(hw[e]);
-            }
-            o[e] = pack_bf16x2(a, b);
-        }
-        // chunks past K hold zeros (x = 0, shift = 0): they add nothing to the maximum
-        v[c] = make_uint4(o[0], o[1], o[2], o[3]);
-        m2 = absmax_bf16x2(m2, v[c].x);
-        m2 = absmax_bf16x2(m2, v[c].y);
-        m2 = absmax_bf16x2(m2, v[c].z);
-        m2 = absmax_bf16x2(m2, v[c].w);
-    }
-    uint4* nr = reinterpret_cast<uint4*>(p.normed + rr * p.ldn);
-    if (!p.y) {                                      // the pre-norm alone (bf16 out)
+        for (int c = 0; c < CPL; ++c)
+            v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, chunk_off(c), 0, kBufferLoadOnce));
+    };
+    float f[CPL][8], h[CPL][8];
+    auto load_factors = [&](int64_t ti) {
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.weight ? p.weight : p.x), 0, p.weight ? rowbytes : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t scs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(AFFINE ? p.mod_scale + ti * p.ldmod : p.x), 0, AFFINE ? rowbytes : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t shs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(AFFINE ? p.mod_shift + ti * p.ldmod : p.x), 0, AFFINE ? rowbytes : 0, 0x00020000);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const int idx = part * kLanes + lane + kLanes * WPR * c;
-            if (valid && idx < nch) store_normed<NT>(nr + idx, v[c]);
+            const uint4 wv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, chunk_off(c), 0, 0));
+            const uint4 sc = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(scs, chunk_off(c), 0, 0));
+            const uint4 sh = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(shs, chunk_off(c), 0, 0));
+            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, sw[4] = {sc.x, sc.y, sc.z, sc.w},
+                           hw[4] = {sh.x, sh.y, sh.z, sh.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float w0 = p.weight ? bf16_lo(ww[e]) : 1.0f, w1 = p.weight ? bf16_hi(ww[e]) : 1.0f;
+                f[c][2 * e] = AFFINE ? w0 * (1.0f + bf16_lo(sw[e])) : w0;
+                f[c][2 * e + 1] = AFFINE ? w1 * (1.0f + bf16_hi(sw[e])) : w1;
+                h[c][2 * e] = AFFINE ? bf16_lo(hw[e]) : 0.0f;
+                h[c][2 * e + 1] = AFFINE ? bf16_hi(hw[e]) : 0.0f;
+            }
         }
-        return;
-    }
-    uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
-    if (WPR > 1) {
-        if (lane == 0) smax[wave] = mbits;
-        __syncthreads();
+    };
+    auto table_row = [&](int64_t row) -> int64_t {
+        if (!AFFINE || !p.mod_index || row >= row_end) return 0;
+        // wave-uniform (one row per wave group): kept in scalar registers, so the
+        // table descriptors are too
+        const int32_t ti = __builtin_amdgcn_readfirstlane(p.mod_index[row]);
+        return min(max((int64_t)ti, (int64_t)0), p.mod_rows - 1);
+    };
+
+    uint4 va[CPL], vb[CPL];
+    load_row(row0, va);
+    int64_t cur_ti = table_row(row0);
+    load_factors(cur_ti);
+    auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL]) {
+        const int64_t row = uniform(row_in);
+        load_row(row + 1, vn);                       // the next row, in flight meanwhile
+        __builtin_amdgcn_sched_barrier(0);
+        const bool valid = row < row_end;
+        if (AFFINE && p.mod_index) {
+            const int64_t ti = table_row(row);
+            if (ti != cur_ti) {                      // wave-uniform: a new frame's table row
+                cur_ti = ti;
+                load_factors(ti);
+            }
+        }
+        // sum of squares straight from the packed bf16 pairs (v_dot2c_f32_bf16: no
+        // unpacking), four partial sums to keep the chains short
+        float ssp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
-    }
-    const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
-    if (valid && part == 0 && lane == 0) p.y_scale[row] = scale;
-    const float r = 1.0f / scale;
-    uint2* yr = reinterpret_cast<uint2*>(p.y + rr * p.ldy);
-    const bool finite = __builtin_isfinite(scale);
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        const int idx = part * kLanes + lane + kLanes * WPR * c;
-        if (!valid || idx >= nch) continue;
-        if (p.normed) store_normed<NT>(nr + idx, v[c]);
-        yr[idx] = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
+            for (int e = 0; e < 4; ++e)
+                ssp[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4[e]),
+                                                         __builtin_bit_cast(bf16x2_t, w4[e]), ssp[e], false);
+        }
+        float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
+        if (WPR > 1) {
+            if (lane == 0) ssum[wave] = ss;
+            __syncthreads();
+            ss = ssum[(wave / WPR) * WPR];
+#pragma unroll
+            for (int w = 1; w < WPR; ++w) ss += ssum[(wave / WPR) * WPR + w];
+        }
+        const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+        uint32_t m2 = 0;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float a = bf16_lo(xw[e]) * rstd, b = bf16_hi(xw[e]) * rstd;
+                if (AFFINE) {
+                    a = __builtin_fmaf(a, f[c][2 * e], h[c][2 * e]);
+                    b = __builtin_fmaf(b, f[c][2 * e + 1], h[c][2 * e + 1]);
+                } else {
+                    a *= f[c][2 * e];
+                    b *= f[c][2 * e + 1];
+                }
+                o[e] = pack_bf16x2(a, b);
+            }
+            // chunks past K hold zeros (x = 0, f = 0, shift = 0): nothing to the maximum
+            v[c] = make_uint4(o[0], o[1], o[2], o[3]);
+            m2 = absmax_bf16x2(m2, v[c].x);
+            m2 = absmax_bf16x2(m2, v[c].y);
+            m2 = absmax_bf16x2(m2, v[c].z);
+            m2 = absmax_bf16x2(m2, v[c].w);
+        }
+        const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.normed ? p.normed + (valid ? row : 0) * p.ldn : nullptr)), 0,
+            (valid && p.normed) ? rowbytes : 0, 0x00020000);
+        if (!QUANT) {                                // the pre-norm alone (bf16 out)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, chunk_off(c), 0,
+                                                       NT ? kBufferLoadOnce : 0);
+            return;
+        }
+        uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+        if (WPR > 1) {
+            if (lane == 0) smax[wave] = mbits;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
+        }
+        const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
+        if (valid && part == 0 && lane == 0) p.y_scale[row] = scale;
+        const float r = 1.0f / scale;
+        const bool finite = __builtin_isfinite(scale);
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.y + (valid ? row : 0) * p.ldy)), 0, valid ? nch * 8 : 0, 0x00020000);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t off = chunk_off(c);
+            if (p.normed)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, off, 0, NT ? kBufferLoadOnce : 0);
+            const uint2 q = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2_t, q), yrs, off / 2, 0, 0);
+        }
+    };
+    for (int64_t i = 0; i < rb; i += 2) {
+        one_row(row0 + i, va, vb);
+        if (i + 1 < rb) one_row(row0 + i + 1, vb, va);
     }
 }
 
@@ -609,24 +654,31 @@ extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K,
 
 namespace vdn {
 namespace {
-// k_norm_quant with WPR waves per row, chunks per lane rounded up to an
-// instantiated count (2..8); false when none covers the row.
-template <int WPR>
-bool launch_norm_multi(int64_t nch, int64_t M, const NormArgs& p, hipStream_t st)
+// k_norm_quant_blocks: WPR waves per row, rows in blocks of rb per wave group,
+// three workgroups per CU; false when no instantiated chunk count covers the row.
+template <int WPR, bool QUANT>
+bool launch_norm_blocks(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStream_t st)
 {
     const bool nt = p.normed && M * nch * 16 >= kNtStoreBytes;   // the normed bf16 output
     const int64_t per = (nch + WPR * kLanes - 1) / (WPR * kLanes);
-    const dim3 grid((unsigned)((M + kWavesPerBlock / WPR - 1) / (kWavesPerBlock / WPR))), block(kWavesPerBlock * kLanes);
-#define VDN_CASE(n)                                                                 \
-    if (per <= n) {                                                                 \
-        if (nt) hipLaunchKernelGGL((k_norm_quant<n, WPR, true>), grid, block, 0, st, p);  \
-        else hipLaunchKernelGGL((k_norm_quant<n, WPR, false>), grid, block, 0, st, p);   \
-        return true;                                                                \
+    const int64_t groups_per_wg = kWavesPerBlock / WPR;
+    const int64_t wgs = min((int64_t)cus * 3, (M + groups_per_wg - 1) / groups_per_wg);
+    const int64_t rb = (M + wgs * groups_per_wg - 1) / (wgs * groups_per_wg);
+    const dim3 grid((unsigned)((M + rb * groups_per_wg - 1) / (rb * groups_per_wg))), block(kWavesPerBlock * kLanes);
+    const bool affine = p.mod_scale != nullptr;
+#define VDN_LAUNCH(n, NT_, AF_) hipLaunchKernelGGL((k_norm_quant_blocks<n, WPR, NT_, AF_, QUANT>), grid, block, 0, st, p, rb)
+#define VDN_CASE(n)                                                          \
+    if (per <= n) {                                                          \
+        if (affine) { if (nt) VDN_LAUNCH(n, true, true); else VDN_LAUNCH(n, false, true); }     \
+        else { if (nt) VDN_LAUNCH(n, true, false); else VDN_LAUNCH(n, false, false); }          \
+        return true;                                                         \
     }
-    VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
+    VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
 #undef VDN_CASE
+#undef VDN_LAUNCH
     return false;
 }
+
 }  // namespace
 }  // namespace vdn
 
@@ -654,25 +706,18 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     if (nch > 32 * kLanes) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: K=%lld above the supported 16384", (long long)K);
     NormArgs p{(const uint16_t*)x, M, K, ldx, (const uint16_t*)weight, eps, (const uint16_t*)mod_scale,
                (const uint16_t*)mod_shift, ldmod, mod_index, mod_rows, (uint8_t*)y, ldy, y_scale, (uint16_t*)normed, ldn};
-    const dim3 block(kWavesPerBlock * kLanes);
-    if (nch > 4 * kLanes) {
-        // rows of more than 2048 elements: two waves per row up to 8192 elements,
-        // four beyond (at most 8 chunks per lane: the weight and table chunks are
-        // held in registers with the row)
-        if (nch <= 16 * kLanes) {
-            if (launch_norm_multi<2>(nch, M, p, stream)) return check_launch("norm_quantize_rows");
-        } else if (launch_norm_multi<4>(nch, M, p, stream)) {
-            return check_launch("norm_quantize_rows");
-        }
-        return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
-    }
-    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
-    switch (pick_cpl(nch)) {
-#define VDN_CASE(n) case n: hipLaunchKernelGGL((k_norm_quant<n, 1, false>), grid, block, 0, stream, p); break;
-        VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4)
-#undef VDN_CASE
-        default: return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
-    }
+    // rows in blocks per wave group; one wave per row up to 2048 elements, two up to
+    // 8192, four beyond
+    const int cus = device_cus();
+    if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "norm_quantize_rows: cannot query the device's compute units");
+    bool ok;
+    if (y) ok = nch <= 4 * kLanes    ? launch_norm_blocks<1, true>(nch, M, p, cus, stream)
+                : nch <= 16 * kLanes ? launch_norm_blocks<2, true>(nch, M, p, cus, stream)
+                                     : launch_norm_blocks<4, true>(nch, M, p, cus, stream);
+    else ok = nch <= 4 * kLanes    ? launch_norm_blocks<1, false>(nch, M, p, cus, stream)
+              : nch <= 16 * kLanes ? launch_norm_blocks<2, false>(nch, M, p, cus, stream)
+                                   : launch_norm_blocks<4, false>(nch, M, p, cus, stream);
+    if (!ok) return set_error(VDN_FP8_EINVAL, "norm_quantize_rows: unsupported K");
     return check_launch("norm_quantize_rows");
 }
 
