@@ -33,6 +33,7 @@
 // the codes 16.
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "vdn_common.h"
@@ -387,6 +388,444 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// One pass: whole rows of W' held in registers (k_lora_rows)
+// ---------------------------------------------------------------------------
+// A workgroup of eight waves owns a group of 32 rows of W and every column. The
+// columns advance in 256-wide chunks; wave w merges columns 32 w .. 32 w + 31 of
+// each chunk for all 32 rows, so a lane (row n = lane % 32, half h = lane / 32)
+// holds 16 consecutive columns of one row per chunk: all of its row's share of
+// W' stays in VGPRs (8 words a chunk, 160 at K = 5120) until the row maximum is
+// known, and W is read from HBM exactly once.
+//
+// The rank-r update is v_mfma_f32_32x32x16_bf16 with MFMA row i = a column of
+// the chunk, MFMA column j = a row n of W, reduction = rank: the B operand
+// (B[n][...]) stays in VGPRs for the whole group, the A operand comes from the
+// chunk's slice of A, staged in LDS in its natural [rank][column] layout and
+// read with ds_read_b64_tr_b16 (gfx950's transposing LDS read: lane i of each
+// 16-lane group receives element i % 4 of the 8-byte row addressed by lane
+// 4 j + i / 4, for j = 0..3), so no transposed copy of A is needed. MFMA row i
+// stands for column 16 ((i / 4) % 2) + 4 (i / 8) + i % 4 of the wave's 32, which
+// makes accumulator r of lane (n, h) column 16 h + r.
+//
+// Both streams reach LDS by global -> LDS copies: W (from HBM) through four
+// 16 KiB stages, A (from L2) through three. Waves 0-3 issue only the W copies
+// and waves 4-7 only the A copies, so each wave's memory counter orders one
+// stream and its waits are exact: the long-latency W stream never holds up the
+// short A stream or the reverse, and the merge of chunk c runs while W of
+// chunks c + 1 .. c + 3 is on its way. After the last chunk the row maxima meet
+// in LDS; the next group's first four W chunks are requested, and the codes
+// leave through LDS (the A stages' space) as whole 1 KiB row pieces, part by
+// part, while those chunks stream in. The grid is persistent, one workgroup
+// per CU.
+namespace rows {
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kLanes;   // 512
+constexpr int kRows = 32;                   // rows of W per group
+constexpr int kChunk = 256;                 // columns per chunk (32 per wave)
+constexpr int kMaxChunks = 20;              // K <= 5120
+constexpr int kWStages = 4;                 // W chunks in LDS (16 KiB each)
+constexpr int kAStages = 3;                 // A slices in LDS (RP x 512 bytes each)
+constexpr int kRowB = kChunk * 2;           // bytes of one row of a chunk (W) or one rank row of a slice (A)
+constexpr int kWStage = kRows * kRowB;      // 16 KiB
+constexpr int kMovers = 4;                  // waves per stream
+}  // namespace rows
+
+struct RowArgs {
+    const uint16_t* w;
+    int64_t N, K, ldw;
+    const uint16_t* a;   // [rank, K], rows K elements apart
+    const uint16_t* b;   // [N, rank]
+    int64_t rank;
+    float lora_scale;
+    uint8_t* wq;         // rows ldq bytes apart, 16-byte aligned
+    int64_t ldq;
+    float* w_scale;
+    uint16_t* w_merged;  // MERGED only: rows ldw apart, 16-byte aligned
+    int nch;             // ceil(K / 256)
+    int groups;          // ceil(N / 32)
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// One wave-wide global -> LDS copy of 16 bytes per lane: lane L's bytes at
+// buffer offset voff land at LDS byte lds + 16 L. Inline assembly, so that the
+// compiler does not make every later LDS read wait for it; the kernel waits on
+// vmcnt itself. M0 carries the LDS address (restored afterwards); s_nop covers
+// the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff)
+{
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rsrc)
+        : "memory");
+}
+
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
+{
+    const uint64_t a = (uint64_t)base;
+    bytes = max(min(bytes, (int64_t)0x7fffffff), (int64_t)0);
+    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu)),
+                   __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// s_waitcnt with vmcnt = VM (63: no condition on memory operations) and
+// lgkmcnt = 0 (this wave's LDS accesses done).
+template <int VM>
+__device__ __forceinline__ void wait_vm_lgkm()
+{
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (0 << 8) | ((VM >> 4) << 14));
+}
+
+// The wait, then all waves meet. The scheduling barriers keep the compiler from
+// moving instructions across.
+template <int VM>
+__device__ __forceinline__ void rows_sync()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm<VM>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// rows_sync<n> for an n known once the chunk loops are unrolled (the counter
+// holds at most 63 operations: more pending after the awaited one means it is
+// done).
+__device__ __forceinline__ void rows_sync_n(int n)
+{
+    switch (n < 63 ? n : 63) {
+#define VDN_SYNC_CASE(V) case V: rows_sync<V>(); break;
+#define VDN_SYNC_CASE8(V) VDN_SYNC_CASE(V) VDN_SYNC_CASE(V + 1) VDN_SYNC_CASE(V + 2) VDN_SYNC_CASE(V + 3) \
+        VDN_SYNC_CASE(V + 4) VDN_SYNC_CASE(V + 5) VDN_SYNC_CASE(V + 6) VDN_SYNC_CASE(V + 7)
+        VDN_SYNC_CASE8(0) VDN_SYNC_CASE8(8) VDN_SYNC_CASE8(16) VDN_SYNC_CASE8(24)
+        VDN_SYNC_CASE8(32) VDN_SYNC_CASE8(40) VDN_SYNC_CASE8(48) VDN_SYNC_CASE8(56)
+#undef VDN_SYNC_CASE8
+#undef VDN_SYNC_CASE
+        default: rows_sync<0>(); break;
+    }
+}
+
+// A 16-byte buffer store, then wait states before anything can overwrite its
+// data registers. Without them the compiler placed a VALU write of the first
+// data register two instructions after such a store, and the store sent the new
+// value for the last four lanes of each 16-lane quarter (seen as wrong codes in
+// the first dword of those lanes).
+__device__ __forceinline__ void store16_settled(i32x4_t v, __amdgpu_buffer_rsrc_t rs, uint32_t off, int soff)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, soff, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int RP, int NCH, bool BVEC, bool MERGED>
+__global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
+{
+    using namespace rows;
+    constexpr int kSteps = RP / 16;                  // rank steps of 16 (one MFMA each)
+    constexpr int kAStage = RP * kRowB;
+    constexpr int kWCopies = kWStage / 1024 / kMovers;  // 1 KiB W copies per W wave per chunk (4)
+    constexpr int kACopies = kAStage / 1024 / kMovers;  // 1 KiB A copies per A wave per chunk (RP / 8)
+    constexpr int kWArea = kWStages * kWStage;
+    constexpr int kAArea = kAStages * kAStage;
+    // The codes leave in parts of kPart chunks, staged by rows in the A area (rows
+    // padded by 16 bytes: the 16 rows one 16-byte write of a quarter-wave covers fall
+    // on 16 different bank quads); the last KiB of the A area holds the row maxima.
+    constexpr int kRedOff = kWArea + kAArea - 1024;
+    constexpr int kPartMax = ((kAArea - 1024) / kRows - 16) / kChunk;
+    constexpr int kPart = kPartMax < NCH ? kPartMax : NCH;
+    constexpr int kParts = (NCH + kPart - 1) / kPart;
+    constexpr int kCRow = kPart * kChunk + 16;
+    static_assert(kPart >= 1 && kRows * kCRow <= kAArea - 1024, "codes staging exceeds the A area");
+    // 16-byte code stores per wave over all parts (rows wave + 8 i, 1 KiB pieces)
+    constexpr int kStorePieces = (kPart * kChunk + 1023) / 1024;
+    constexpr int kLastPart = NCH - (kParts - 1) * kPart;
+    constexpr int kLastPieces = (kLastPart * kChunk + 1023) / 1024;
+    constexpr int kStores = (kRows / rows::kWaves) * ((kParts - 1) * kStorePieces + kLastPieces) + (MERGED ? 2 * NCH : 0);
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kWArea + kAArea];
+    uint32_t* const red = reinterpret_cast<uint32_t*>(smem + kRedOff);
+
+    const int tid = threadIdx.x, lane = tid & (kLanes - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nl = lane & 31, h = lane >> 5;
+    const bool wmover = wave < kMovers;               // waves 0-3 copy W, 4-7 copy A
+    const int mv = wave & (kMovers - 1);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+
+    // Copy i of a W wave moves rows 2 d and 2 d + 1 (d = 4 mv + i) of a chunk; lane L
+    // fills row 2 d + L / 32, 16-byte piece L % 32, which holds the row's logical
+    // piece (L % 32) ^ (row % 16): the 16 rows a quarter-wave reads at one column
+    // fall on 16 different bank quads. Copy i of an A wave moves rank rows 2 d and
+    // 2 d + 1 (d = kACopies mv + i) of a slice, piece (L % 32) ^ (4 (row % 4)): the
+    // four rank rows of one transposing read sit in four different 64-byte windows.
+    // (The lane-dependent offsets are formed where they are used, from opaque
+    // copies: kept for every copy they would hold registers throughout.)
+    const i32x4_t arsrc = rsrc_words(p.a, p.rank * p.K * 2);
+    auto copy_w = [&](i32x4_t wrs, int c, int st) {
+#pragma unroll
+        for (int i = 0; i < kWCopies; ++i) {
+            int l = lane;
+            asm volatile("" : "+v"(l));
+            const int row = 2 * (kWCopies * mv + i) + (l >> 5);
+            const int lc = (l & 31) ^ (row & 15);
+            copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + (kWCopies * mv + i) * 1024),
+                          (uint32_t)((row * p.ldw + 8 * lc) * 2 + c * kRowB));
+        }
+    };
+    auto copy_a = [&](int c, int st) {
+#pragma unroll
+        for (int i = 0; i < kACopies; ++i) {
+            int l = lane;
+            asm volatile("" : "+v"(l));
+            const int rho = 2 * (kACopies * mv + i) + (l >> 5);
+            const int lc = (l & 31) ^ (4 * (rho & 3));
+            copy16_to_lds(arsrc, lds_base + (uint32_t)(kWArea + st * kAStage + (kACopies * mv + i) * 1024),
+                          (uint32_t)((rho * p.K + 8 * lc) * 2 + c * kRowB));
+        }
+    };
+    // W descriptor of a group (empty past the last group: reads zeros, touches no memory)
+    auto w_rsrc = [&](int64_t n0) {
+        const int64_t rows = n0 < p.N ? min(p.N - n0, (int64_t)kRows) : 0;
+        return rsrc_words(p.w + n0 * p.ldw, rows * p.ldw * 2);
+    };
+    // Transposing reads: lane (group G = lane / 16, j = (lane / 4) % 4, q = lane % 4)
+    // addresses rank row 8 h + j (+ 16 s + 4 half) at the four columns MFMA rows
+    // 16 (G % 2) + 4 q .. + 3 stand for: 32 wave + 16 (q % 2) + 8 (G % 2) + 4 (q / 2).
+    const int tj = (lane >> 2) & 3, tq = lane & 3, tg = (lane >> 4) & 1;
+    const uint32_t tr_off = (uint32_t)((8 * h + tj) * kRowB +
+                                       (((4 * wave + 2 * (tq & 1) + tg) ^ (4 * tj)) << 4) + 8 * (tq >> 1));
+    // This lane's W pieces in a stage: row n, logical pieces 4 wave + 2 h + e.
+    const uint32_t wrd0 = (uint32_t)(nl * kRowB + (((4 * wave + 2 * h) ^ (nl & 15)) << 4));
+    const uint32_t wrd1 = (uint32_t)(nl * kRowB + (((4 * wave + 2 * h + 1) ^ (nl & 15)) << 4));
+
+    const int lcol = 32 * wave + 16 * h;                       // first column of the lane in a chunk
+    const int nvalid = (int)((p.K - lcol + kChunk - 1) / kChunk);   // chunks with this lane's columns < K
+    auto col_in = [&](int c) {
+        int nv = nvalid;
+        asm volatile("" : "+v"(nv));
+        return c < nv;
+    };
+    auto voff_at = [&](uint32_t base, int c) {
+        asm volatile("" : "+v"(base));
+        return col_in(c) ? base : kDropped;
+    };
+
+    // B operand of rank step s: B[n][16 s + 8 h .. + 7], zero beyond the rank; the
+    // raw 16-byte loads are masked where they are first used.
+    bf16x8_t braw[kSteps];
+    auto load_b = [&](int64_t n0) {
+        const int64_t rows = n0 < p.N ? min(p.N - n0, (int64_t)kRows) : 0;
+        const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.b + n0 * p.rank), 0, (int)(rows * p.rank * 2), 0x00020000);
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s)
+            braw[s] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                br, (uint32_t)((nl * p.rank + 16 * s + 8 * h) * 2), 0, 0));
+    };
+
+    int g = blockIdx.x;
+    if (g >= p.groups) return;
+    // Prologue of the first group: B, then the first W chunks (W waves) or A slices (A waves).
+    load_b((int64_t)g * kRows);
+    {
+        const i32x4_t wrs = w_rsrc((int64_t)g * kRows);
+        if (wmover) {
+#pragma unroll
+            for (int c = 0; c < kWStages; ++c) copy_w(wrs, c, c);
+        } else {
+#pragma unroll
+            for (int c = 0; c < kAStages; ++c) copy_a(c, c);
+        }
+    }
+
+    uint32_t wr[NCH][8];
+    bool first = true;
+    for (; g < p.groups; g += gridDim.x) {
+        const int64_t n0 = (int64_t)g * kRows;
+        const int64_t rows = min(p.N - n0, (int64_t)kRows);
+        const i32x4_t wrs = w_rsrc(n0);
+        bf16x8_t bop[kSteps];
+
+        // Merge: W' = bf16(W + bf16(scale * B A)) per chunk, into wr[c]; mx keeps the
+        // packed bf16 magnitude maximum of the valid columns.
+        uint32_t mx = 0u;
+        auto merge_chunk = [&](int c) {
+            // Chunk c has landed once only the later memory operations of this wave
+            // may be pending. A W wave has then issued chunks up to c + kWStages - 2
+            // (chunk c + kWStages - 1 goes out after this wait), an A wave slices up
+            // to c + kAStages - 2; the first kWStages chunks (W) and kAStages slices
+            // (A) of every group but the first were requested while the previous
+            // group's codes went out, so that group's code stores (W waves) and this
+            // group's B loads (both) come after them as well.
+            if (wmover) {
+                const int later = c == 0 ? kWStages - 1 : min(kWStages - 2, NCH - 1 - c);
+                rows_sync_n(kWCopies * later + ((c < kWStages && !first) ? kStores + kSteps : 0));
+            } else {
+                const int later = c == 0 ? kAStages - 1 : min(kAStages - 2, NCH - 1 - c);
+                rows_sync_n(kACopies * later + ((c < kAStages && !first) ? kSteps : 0));
+            }
+            if (c == 0) {
+                // (masked past the first wait: the B loads are long done by then)
+#pragma unroll
+                for (int s = 0; s < kSteps; ++s)
+                    bop[s] = (!BVEC || 16 * s + 8 * h < p.rank) ? braw[s] : bf16x8_t{};
+            }
+            // every wave is past chunk c - 1: its stages can take chunk c + kWStages - 1
+            // (W) and slice c + kAStages - 1 (A)
+            if (wmover) {
+                if (c + kWStages - 1 < NCH && c >= 1) copy_w(wrs, c + kWStages - 1, (c + kWStages - 1) % kWStages);
+            } else {
+                if (c + kAStages - 1 < NCH && c >= 1) copy_a(c + kAStages - 1, (c + kAStages - 1) % kAStages);
+            }
+            // this lane's W pieces
+            {
+                const uint8_t* ws = smem + (c % kWStages) * kWStage;
+                const uint4 x = *reinterpret_cast<const uint4*>(ws + wrd0);
+                const uint4 y = *reinterpret_cast<const uint4*>(ws + wrd1);
+                wr[c][0] = x.x; wr[c][1] = x.y; wr[c][2] = x.z; wr[c][3] = x.w;
+                wr[c][4] = y.x; wr[c][5] = y.y; wr[c][6] = y.z; wr[c][7] = y.w;
+            }
+            const uint8_t* st = smem + kWArea + (c % kAStages) * kAStage + tr_off;
+            f32x16_t acc = f32x16_t{};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+                const lds_s16x4_t* p0 = (const lds_s16x4_t*)(lds_void_t*)(st + (16 * s) * kRowB);
+                const lds_s16x4_t* p1 = (const lds_s16x4_t*)(lds_void_t*)(st + (16 * s + 4) * kRowB);
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p0));
+                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p1));
+                const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, (short __attribute__((ext_vector_type(8)))){
+                    lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[s], acc, 0, 0, 0);
+            }
+            uint32_t gm = 0u;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                uint32_t dl = pack_bf16x2(acc[2 * d] * p.lora_scale, acc[2 * d + 1] * p.lora_scale);
+                asm volatile("" : "+v"(dl));
+                uint32_t m = pack_bf16x2(bf16_lo(wr[c][d]) + bf16_lo(dl), bf16_hi(wr[c][d]) + bf16_hi(dl));
+                asm volatile("" : "+v"(m));
+                wr[c][d] = m;
+                gm = absmax_bf16x2(gm, m);
+            }
+            mx = col_in(c) ? absmax_bf16x2(mx, gm) : mx;
+        };
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) merge_chunk(c);
+
+        // Row maxima: the two halves of each lane's words, the two lanes of a row,
+        // then the eight waves through LDS (in the last KiB of the A area: written
+        // once every wave is done with the last chunk).
+        uint32_t m16 = max(mx & 0xffffu, mx >> 16);
+        m16 = max(m16, (uint32_t)__shfl_xor((int)m16, 32, 64));
+        rows_sync<63>();
+        if (h == 0) red[wave * kRows + nl] = m16;
+        rows_sync<63>();
+        uint32_t mbits = 0u;
+#pragma unroll
+        for (int w8 = 0; w8 < rows::kWaves; ++w8) mbits = max(mbits, red[w8 * kRows + nl]);
+        const float s32 = row_scale(bf16_to_f32((uint16_t)mbits));
+        {
+            const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.w_scale + n0), 0, (int)(rows * 4), 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s32), sr,
+                                                  (wave == 0 && h == 0) ? (uint32_t)(nl * 4) : kDropped, 0, 0);
+        }
+        const float sb = round_bf16(s32);
+        const float r = 1.0f / sb;
+        // every wave holds the same 32 rows: the branch is uniform over the workgroup
+        const bool exact = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(sb)) != 0;
+
+        // The next group's first W chunks (the W stages are free: every wave has read
+        // its last chunk), then the codes, part by part.
+        const int gn = g + (int)gridDim.x;
+        const bool more = gn < p.groups;
+        const i32x4_t nrs = w_rsrc((int64_t)gn * kRows);
+        if (wmover) {
+#pragma unroll
+            for (int c = 0; c < kWStages; ++c) copy_w(nrs, c, c);
+        }
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.wq + n0 * p.ldq), 0, (int)(rows * p.ldq), 0x00020000);
+        const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(MERGED ? p.w_merged + n0 * p.ldw : nullptr), 0, MERGED ? (int)(rows * p.ldw * 2) : 0, 0x00020000);
+        uint8_t* const cst = smem + kWArea;
+        // (one uniform branch per chunk around the quotients only)
+        auto codes_chunk = [&](int c, int c0) {
+            uint32_t q[4];
+            if (exact) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint2 v = make_uint2(wr[c][2 * i], wr[c][2 * i + 1]);
+                    // opaque, so that the compiler does not unpack every word once for
+                    // both paths ahead of the branch
+                    asm volatile("" : "+v"(v.x), "+v"(v.y));
+                    q[i] = codes4_exact(v, sb);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) q[i] = codes4(make_uint2(wr[c][2 * i], wr[c][2 * i + 1]), r);
+            }
+            *reinterpret_cast<uint4*>(cst + nl * kCRow + (c - c0) * kChunk + lcol) = make_uint4(q[0], q[1], q[2], q[3]);
+            if (MERGED) {
+                const uint32_t wv = (uint32_t)((nl * p.ldw + lcol) * 2);
+                const uint32_t off = voff_at(wv, c);
+                store16_settled(u32x4(wr[c][0], wr[c][1], wr[c][2], wr[c][3]), mr, off, c * kRowB);
+                store16_settled(u32x4(wr[c][4], wr[c][5], wr[c][6], wr[c][7]), mr, off + 16, c * kRowB);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Rows wave + 8 i of a part, 1 KiB (64 lanes x 16 bytes) per store; columns past
+        // K and rows past N go out of range.
+        auto store_part = [&](int c0, int nc) {
+            const int bytes = nc * kChunk;
+#pragma unroll
+            for (int i = 0; i < kRows / rows::kWaves; ++i) {
+                const int row = wave + rows::kWaves * i;
+#pragma unroll
+                for (int j = 0; j < kStorePieces; ++j) {
+                    const int b = 1024 * j + 16 * lane;
+                    if (1024 * j < bytes) {
+                        const uint4 v = *reinterpret_cast<const uint4*>(cst + row * kCRow + min(b, bytes - 16));
+                        const int64_t col = (int64_t)c0 * kChunk + b;
+                        const uint32_t off = (b < bytes && col < p.K) ? (uint32_t)(row * p.ldq + b) : kDropped;
+                        store16_settled(__builtin_bit_cast(i32x4_t, v), qr, off, c0 * kChunk);
+                    }
+                }
+            }
+        };
+#pragma unroll
+        for (int part = 0; part < kParts; ++part) {
+            const int c0 = part * kPart;
+            const int nc = part + 1 < kParts ? kPart : kLastPart;
+#pragma unroll
+            for (int c = c0; c < c0 + nc; ++c) codes_chunk(c, c0);
+            rows_sync<63>();
+            store_part(c0, nc);
+            rows_sync<63>();
+        }
+        // The next group's first A slices (the A area is free again) and B rows.
+        if (more && !wmover) {
+#pragma unroll
+            for (int c = 0; c < kAStages; ++c) copy_a(c, c);
+        }
+        load_b((int64_t)gn * kRows);
+        first = false;
+    }
+    // No copy may still be writing LDS when the workgroup ends.
+    wait_vm_lgkm<0>();
+}
+
 __global__ void k_zero_u32(uint32_t* x, int64_t n)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -464,6 +903,38 @@ int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, co
     const int wm16 = w_merged && ((uintptr_t)w_merged % 16 == 0);
     const int cus = device_cus();
     if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "requantize_weight: cannot query the device's compute units");
+    // One pass with the rows in registers: codes wanted, rank <= 64 with 16-byte B
+    // rows, K <= 5120, 16-byte rows everywhere.
+    const bool one_pass = !merge_only && rank <= 64 && b_vec && K <= (int64_t)rows::kChunk * rows::kMaxChunks &&
+                          aligned(w, 16) && ldw % 8 == 0 && aligned(wq, 16) && ldq % 16 == 0 &&
+                          (!w_merged || aligned(w_merged, 16)) && (int64_t)rows::kRows * ldw * 2 <= 0x7fffffffLL &&
+                          (int64_t)rows::kRows * ldq <= 0x7fffffffLL && rank * K * 2 <= 0x7fffffffLL;
+    if (one_pass) {
+        RowArgs r{w, N, K, ldw, a, b, rank, lora_scale, wq, ldq, w_scale, w_merged,
+                  (int)((K + rows::kChunk - 1) / rows::kChunk), (int)((N + rows::kRows - 1) / rows::kRows)};
+        // persistent grid: as many rounds of groups as the CUs need, the groups spread
+        // evenly over the workgroups (480 groups on 256 CUs: 240 workgroups of two)
+        const int64_t rounds = (r.groups + cus - 1) / cus;
+        const dim3 grid((unsigned)((r.groups + rounds - 1) / rounds)), block(rows::kThreads);
+        // chunk-count instances: 8 (K <= 2048), 16 (K <= 4096), 20 (K <= 5120); chunks past
+        // K read nothing and store nothing
+#define VDN_LORA_ROWS(R, C)                                                                            \
+    do {                                                                                               \
+        if (w_merged) hipLaunchKernelGGL((k_lora_rows<R, C, true, true>), grid, block, 0, stream, r);  \
+        else hipLaunchKernelGGL((k_lora_rows<R, C, true, false>), grid, block, 0, stream, r);          \
+    } while (0)
+#define VDN_LORA_ROWS_RP(R)                              \
+    do {                                                 \
+        if (r.nch <= 8) VDN_LORA_ROWS(R, 8);             \
+        else if (r.nch <= 16) VDN_LORA_ROWS(R, 16);      \
+        else VDN_LORA_ROWS(R, 20);                       \
+    } while (0)
+        if (rank <= 32) VDN_LORA_ROWS_RP(32);
+        else VDN_LORA_ROWS_RP(64);
+#undef VDN_LORA_ROWS_RP
+#undef VDN_LORA_ROWS
+        return check_launch("requantize_weight (LoRA, one pass)");
+    }
     Args p{w, N, K, ldw, a, b, rank, b_vec, lora_scale, wq, ldq, w_scale, w_merged, wm16,
            (int)((K + kTileCols - 1) / kTileCols), (int)((N + kTileRows - 1) / kTileRows)};
     const int rp = (int)((rank + 31) / 32) * 32;
