@@ -35,6 +35,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "vdn_common.h"
 
@@ -409,11 +410,12 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
 // makes accumulator r of lane (n, h) column 16 h + r.
 //
 // Both streams reach LDS by global -> LDS copies: W (from HBM) through four
-// 16 KiB stages, A (from L2) through three. Waves 0-3 issue only the W copies
-// and waves 4-7 only the A copies, so each wave's memory counter orders one
-// stream and its waits are exact: the long-latency W stream never holds up the
-// short A stream or the reverse, and the merge of chunk c runs while W of
-// chunks c + 1 .. c + 3 is on its way. After the last chunk the row maxima meet
+// 16 KiB stages, A (from L2) through three; every wave issues its share of both
+// (2 W and RP / 16 A copies of 1 KiB per chunk). A wave's memory counter orders
+// its operations as issued, so slice c of A is requested after chunk c of W and
+// before chunk c + 1: one exact wait for slice c then covers both, while W of
+// chunks c + 1 and c + 2 stays in flight (chunk c + 3 goes out after it), and
+// the merge of chunk c runs meanwhile. After the last chunk the row maxima meet
 // in LDS; the next group's first four W chunks are requested, and the codes
 // leave through LDS (the A stages' space) as whole 1 KiB row pieces, part by
 // part, while those chunks stream in. The grid is persistent, one workgroup
@@ -428,7 +430,35 @@ constexpr int kWStages = 4;                 // W chunks in LDS (16 KiB each)
 constexpr int kAStages = 3;                 // A slices in LDS (RP x 512 bytes each)
 constexpr int kRowB = kChunk * 2;           // bytes of one row of a chunk (W) or one rank row of a slice (A)
 constexpr int kWStage = kRows * kRowB;      // 16 KiB
-constexpr int kMovers = 4;                  // waves per stream
+
+// Memory operations a wave has issued after slice c of A by the time it waits
+// for chunk c (wc W copies and ac A copies per chunk, nb B loads per group).
+// Order: in the first group W0 A0 W1 A1 W2 A2 W3; in later groups, requested
+// while the previous group's codes went out, W0-W3, the code stores, A0-A2,
+// the B loads; then, after the wait of each chunk k >= 1, A(k + 2) and W(k + 3).
+constexpr int ops_after_a(int c, bool first, int nch, int wc, int ac, int nb)
+{
+    int count = 0;
+    bool seen = false;
+    auto op = [&](bool is_a, int idx, int n) {
+        if (seen) count += n;
+        if (is_a && idx == c) seen = true;
+    };
+    if (first) {
+        for (int k = 0; k < kWStages && k < nch; ++k) {
+            op(false, k, wc);
+            if (k < kAStages) op(true, k, ac);
+        }
+    } else {
+        for (int k = 0; k < kAStages && k < nch; ++k) op(true, k, ac);
+        op(false, -1, nb);
+    }
+    for (int k = 1; k < c; ++k) {
+        if (k + kAStages - 1 < nch) op(true, k + kAStages - 1, ac);
+        if (k + kWStages - 1 < nch) op(false, k + kWStages - 1, wc);
+    }
+    return count;
+}
 }  // namespace rows
 
 struct RowArgs {
@@ -498,21 +528,17 @@ __device__ __forceinline__ void rows_sync()
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// rows_sync<n> for an n known once the chunk loops are unrolled (the counter
-// holds at most 63 operations: more pending after the awaited one means it is
-// done).
-__device__ __forceinline__ void rows_sync_n(int n)
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, unrolled at compile time
+// (the chunk index is then a constant expression, e.g. for a wait's count).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>)
 {
-    switch (n < 63 ? n : 63) {
-#define VDN_SYNC_CASE(V) case V: rows_sync<V>(); break;
-#define VDN_SYNC_CASE8(V) VDN_SYNC_CASE(V) VDN_SYNC_CASE(V + 1) VDN_SYNC_CASE(V + 2) VDN_SYNC_CASE(V + 3) \
-        VDN_SYNC_CASE(V + 4) VDN_SYNC_CASE(V + 5) VDN_SYNC_CASE(V + 6) VDN_SYNC_CASE(V + 7)
-        VDN_SYNC_CASE8(0) VDN_SYNC_CASE8(8) VDN_SYNC_CASE8(16) VDN_SYNC_CASE8(24)
-        VDN_SYNC_CASE8(32) VDN_SYNC_CASE8(40) VDN_SYNC_CASE8(48) VDN_SYNC_CASE8(56)
-#undef VDN_SYNC_CASE8
-#undef VDN_SYNC_CASE
-        default: rows_sync<0>(); break;
-    }
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // A 16-byte buffer store, then wait states before anything can overwrite its
@@ -534,8 +560,8 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     using namespace rows;
     constexpr int kSteps = RP / 16;                  // rank steps of 16 (one MFMA each)
     constexpr int kAStage = RP * kRowB;
-    constexpr int kWCopies = kWStage / 1024 / kMovers;  // 1 KiB W copies per W wave per chunk (4)
-    constexpr int kACopies = kAStage / 1024 / kMovers;  // 1 KiB A copies per A wave per chunk (RP / 8)
+    constexpr int kWCopies = kWStage / 1024 / rows::kWaves;  // 1 KiB W copies per wave per chunk (2)
+    constexpr int kACopies = kAStage / 1024 / rows::kWaves;  // 1 KiB A copies per wave per chunk (RP / 16)
     constexpr int kWArea = kWStages * kWStage;
     constexpr int kAArea = kAStages * kAStage;
     // The codes leave in parts of kPart chunks, staged by rows in the A area (rows
@@ -558,28 +584,30 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     const int tid = threadIdx.x, lane = tid & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nl = lane & 31, h = lane >> 5;
-    const bool wmover = wave < kMovers;               // waves 0-3 copy W, 4-7 copy A
-    const int mv = wave & (kMovers - 1);
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
 
-    // Copy i of a W wave moves rows 2 d and 2 d + 1 (d = 4 mv + i) of a chunk; lane L
+    // Copy i of a wave's W share moves rows 2 d and 2 d + 1 (d = 2 wave + i) of a chunk; lane L
     // fills row 2 d + L / 32, 16-byte piece L % 32, which holds the row's logical
     // piece (L % 32) ^ (row % 16): the 16 rows a quarter-wave reads at one column
-    // fall on 16 different bank quads. Copy i of an A wave moves rank rows 2 d and
-    // 2 d + 1 (d = kACopies mv + i) of a slice, piece (L % 32) ^ (4 (row % 4)): the
+    // fall on 16 different bank quads. Copy i of its A share moves rank rows 2 d and
+    // 2 d + 1 (d = kACopies wave + i) of a slice, piece (L % 32) ^ (4 (row % 4)): the
     // four rank rows of one transposing read sit in four different 64-byte windows.
     // (The lane-dependent offsets are formed where they are used, from opaque
     // copies: kept for every copy they would hold registers throughout.)
     const i32x4_t arsrc = rsrc_words(p.a, p.rank * p.K * 2);
+    // (The row of copy i is 2 d + h with 2 d even, so its low bits are those of 2 d
+    // or'ed with h: the lane-dependent part of every offset is h times a row plus
+    // a 16-byte piece, the rest is uniform.)
+    const uint32_t ldw2 = (uint32_t)(p.ldw * 2), k2 = (uint32_t)(p.K * 2);
     auto copy_w = [&](i32x4_t wrs, int c, int st) {
 #pragma unroll
         for (int i = 0; i < kWCopies; ++i) {
             int l = lane;
             asm volatile("" : "+v"(l));
-            const int row = 2 * (kWCopies * mv + i) + (l >> 5);
-            const int lc = (l & 31) ^ (row & 15);
-            copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + (kWCopies * mv + i) * 1024),
-                          (uint32_t)((row * p.ldw + 8 * lc) * 2 + c * kRowB));
+            const int d = kWCopies * wave + i, hh = l >> 5;
+            const int lc = (l & 31) ^ (((2 * d) & 15) | hh);
+            copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + d * 1024),
+                          (uint32_t)hh * ldw2 + (uint32_t)(lc << 4) + (uint32_t)(2 * d) * ldw2 + (uint32_t)(c * kRowB));
         }
     };
     auto copy_a = [&](int c, int st) {
@@ -587,10 +615,10 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         for (int i = 0; i < kACopies; ++i) {
             int l = lane;
             asm volatile("" : "+v"(l));
-            const int rho = 2 * (kACopies * mv + i) + (l >> 5);
-            const int lc = (l & 31) ^ (4 * (rho & 3));
-            copy16_to_lds(arsrc, lds_base + (uint32_t)(kWArea + st * kAStage + (kACopies * mv + i) * 1024),
-                          (uint32_t)((rho * p.K + 8 * lc) * 2 + c * kRowB));
+            const int d = kACopies * wave + i, hh = l >> 5;
+            const int lc = (l & 31) ^ (4 * (((2 * d) & 3) | hh));
+            copy16_to_lds(arsrc, lds_base + (uint32_t)(kWArea + st * kAStage + d * 1024),
+                          (uint32_t)hh * k2 + (uint32_t)(lc << 4) + (uint32_t)(2 * d) * k2 + (uint32_t)(c * kRowB));
         }
     };
     // W descriptor of a group (empty past the last group: reads zeros, touches no memory)
@@ -605,8 +633,8 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     const uint32_t tr_off = (uint32_t)((8 * h + tj) * kRowB +
                                        (((4 * wave + 2 * (tq & 1) + tg) ^ (4 * tj)) << 4) + 8 * (tq >> 1));
     // This lane's W pieces in a stage: row n, logical pieces 4 wave + 2 h + e.
+    // (piece 4 wave + 2 h + 1 sits at the other 16 bytes of the pair: 4 wave + 2 h is even)
     const uint32_t wrd0 = (uint32_t)(nl * kRowB + (((4 * wave + 2 * h) ^ (nl & 15)) << 4));
-    const uint32_t wrd1 = (uint32_t)(nl * kRowB + (((4 * wave + 2 * h + 1) ^ (nl & 15)) << 4));
 
     const int lcol = 32 * wave + 16 * h;                       // first column of the lane in a chunk
     const int nvalid = (int)((p.K - lcol + kChunk - 1) / kChunk);   // chunks with this lane's columns < K
@@ -635,16 +663,14 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
 
     int g = blockIdx.x;
     if (g >= p.groups) return;
-    // Prologue of the first group: B, then the first W chunks (W waves) or A slices (A waves).
+    // Prologue of the first group: B, then W0 A0 W1 A1 W2 A2 W3.
     load_b((int64_t)g * kRows);
     {
         const i32x4_t wrs = w_rsrc((int64_t)g * kRows);
-        if (wmover) {
 #pragma unroll
-            for (int c = 0; c < kWStages; ++c) copy_w(wrs, c, c);
-        } else {
-#pragma unroll
-            for (int c = 0; c < kAStages; ++c) copy_a(c, c);
+        for (int c = 0; c < kWStages && c < NCH; ++c) {
+            copy_w(wrs, c, c);
+            if (c < kAStages) copy_a(c, c);
         }
     }
 
@@ -657,61 +683,60 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         bf16x8_t bop[kSteps];
 
         // Merge: W' = bf16(W + bf16(scale * B A)) per chunk, into wr[c]; mx keeps the
-        // packed bf16 magnitude maximum of the valid columns.
+        // packed bf16 magnitude maximum of the valid columns. Software-pipelined by one
+        // chunk: chunk c's LDS reads go out, then chunk c - 1's VALU work (its MFMAs
+        // have had a chunk's time to finish) hides their latency, then chunk c's MFMAs
+        // run while the next chunk waits for its data.
         uint32_t mx = 0u;
-        auto merge_chunk = [&](int c) {
-            // Chunk c has landed once only the later memory operations of this wave
-            // may be pending. A W wave has then issued chunks up to c + kWStages - 2
-            // (chunk c + kWStages - 1 goes out after this wait), an A wave slices up
-            // to c + kAStages - 2; the first kWStages chunks (W) and kAStages slices
-            // (A) of every group but the first were requested while the previous
-            // group's codes went out, so that group's code stores (W waves) and this
-            // group's B loads (both) come after them as well.
-            if (wmover) {
-                const int later = c == 0 ? kWStages - 1 : min(kWStages - 2, NCH - 1 - c);
-                rows_sync_n(kWCopies * later + ((c < kWStages && !first) ? kStores + kSteps : 0));
-            } else {
-                const int later = c == 0 ? kAStages - 1 : min(kAStages - 2, NCH - 1 - c);
-                rows_sync_n(kACopies * later + ((c < kAStages && !first) ? kSteps : 0));
-            }
+        f32x16_t acc;   // chunk c's sums, read by back(c) before mfmas(c + 1) rewrites them
+        auto front = [&](int c) {
             if (c == 0) {
                 // (masked past the first wait: the B loads are long done by then)
 #pragma unroll
                 for (int s = 0; s < kSteps; ++s)
                     bop[s] = (!BVEC || 16 * s + 8 * h < p.rank) ? braw[s] : bf16x8_t{};
             }
-            // every wave is past chunk c - 1: its stages can take chunk c + kWStages - 1
-            // (W) and slice c + kAStages - 1 (A)
-            if (wmover) {
-                if (c + kWStages - 1 < NCH && c >= 1) copy_w(wrs, c + kWStages - 1, (c + kWStages - 1) % kWStages);
-            } else {
-                if (c + kAStages - 1 < NCH && c >= 1) copy_a(c + kAStages - 1, (c + kAStages - 1) % kAStages);
-            }
-            // this lane's W pieces
-            {
-                const uint8_t* ws = smem + (c % kWStages) * kWStage;
-                const uint4 x = *reinterpret_cast<const uint4*>(ws + wrd0);
-                const uint4 y = *reinterpret_cast<const uint4*>(ws + wrd1);
-                wr[c][0] = x.x; wr[c][1] = x.y; wr[c][2] = x.z; wr[c][3] = x.w;
-                wr[c][4] = y.x; wr[c][5] = y.y; wr[c][6] = y.z; wr[c][7] = y.w;
-            }
+        };
+        auto reads_w = [&](int c) {
+            const uint8_t* ws = smem + (c % kWStages) * kWStage;
+            const uint4 x = *reinterpret_cast<const uint4*>(ws + wrd0);
+            const uint4 y = *reinterpret_cast<const uint4*>(ws + (wrd0 ^ 16u));
+            wr[c][0] = x.x; wr[c][1] = x.y; wr[c][2] = x.z; wr[c][3] = x.w;
+            wr[c][4] = y.x; wr[c][5] = y.y; wr[c][6] = y.z; wr[c][7] = y.w;
+        };
+        // the A operand of rank steps s0 .. s1 - 1
+        auto reads_a = [&](int c, bf16x8_t (&aop)[kSteps], int s0, int s1) {
             const uint8_t* st = smem + kWArea + (c % kAStages) * kAStage + tr_off;
-            f32x16_t acc = f32x16_t{};
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
+                if (s < s0 || s >= s1) continue;
                 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
                 const lds_s16x4_t* p0 = (const lds_s16x4_t*)(lds_void_t*)(st + (16 * s) * kRowB);
                 const lds_s16x4_t* p1 = (const lds_s16x4_t*)(lds_void_t*)(st + (16 * s + 4) * kRowB);
                 const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p0));
                 const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p1));
-                const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, (short __attribute__((ext_vector_type(8)))){
+                aop[s] = __builtin_bit_cast(bf16x8_t, (short __attribute__((ext_vector_type(8)))){
                     lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[s], acc, 0, 0, 0);
             }
+        };
+        auto mfmas = [&](int c, const bf16x8_t (&aop)[kSteps]) {
+            f32x16_t a = f32x16_t{};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[s], bop[s], a, 0, 0, 0);
+            acc = a;
+        };
+        auto copies = [&](int c) {
+            // Every wave is past chunk c - 1, so its stages can take chunk
+            // c + kWStages - 1 (W) and slice c + kAStages - 1 (A).
+            if (c >= 1 && c + kAStages - 1 < NCH) copy_a(c + kAStages - 1, (c + kAStages - 1) % kAStages);
+            if (c >= 1 && c + kWStages - 1 < NCH) copy_w(wrs, c + kWStages - 1, (c + kWStages - 1) % kWStages);
+        };
+        auto back = [&](int c) {
+            const f32x16_t& a = acc;
             uint32_t gm = 0u;
 #pragma unroll
             for (int d = 0; d < 8; ++d) {
-                uint32_t dl = pack_bf16x2(acc[2 * d] * p.lora_scale, acc[2 * d + 1] * p.lora_scale);
+                uint32_t dl = pack_bf16x2(a[2 * d] * p.lora_scale, a[2 * d + 1] * p.lora_scale);
                 asm volatile("" : "+v"(dl));
                 uint32_t m = pack_bf16x2(bf16_lo(wr[c][d]) + bf16_lo(dl), bf16_hi(wr[c][d]) + bf16_hi(dl));
                 asm volatile("" : "+v"(m));
@@ -720,8 +745,30 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             }
             mx = col_in(c) ? absmax_bf16x2(mx, gm) : mx;
         };
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) merge_chunk(c);
+        static_for<NCH>([&](auto ic) {
+            constexpr int c = decltype(ic)::value;
+            // Slice c (and with it chunk c, requested before it) has landed once only
+            // the operations issued after it may be pending.
+            constexpr int kFirst = ops_after_a(c, true, NCH, kWCopies, kACopies, kSteps);
+            constexpr int kLater = ops_after_a(c, false, NCH, kWCopies, kACopies, kSteps);
+            if (first) rows_sync<(kFirst > 63 ? 63 : kFirst)>();
+            else rows_sync<(kLater > 63 ? 63 : kLater)>();
+            front(c);
+            // (half of the A operand before the VALU work, half after: all of it held
+            // across that work would cost registers the rows of W' need)
+            bf16x8_t aop[kSteps];
+            reads_w(c);
+            reads_a(c, aop, 0, kSteps / 2);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c >= 1) back(c - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            reads_a(c, aop, kSteps / 2, kSteps);
+            mfmas(c, aop);
+            __builtin_amdgcn_sched_barrier(0);
+            copies(c);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        back(NCH - 1);
 
         // Row maxima: the two halves of each lane's words, the two lanes of a row,
         // then the eight waves through LDS (in the last KiB of the A area: written
@@ -751,10 +798,8 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         const int gn = g + (int)gridDim.x;
         const bool more = gn < p.groups;
         const i32x4_t nrs = w_rsrc((int64_t)gn * kRows);
-        if (wmover) {
 #pragma unroll
-            for (int c = 0; c < kWStages; ++c) copy_w(nrs, c, c);
-        }
+        for (int c = 0; c < kWStages && c < NCH; ++c) copy_w(nrs, c, c);
         const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(p.wq + n0 * p.ldq), 0, (int)(rows * p.ldq), 0x00020000);
         const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(
@@ -815,9 +860,9 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             rows_sync<63>();
         }
         // The next group's first A slices (the A area is free again) and B rows.
-        if (more && !wmover) {
+        if (more) {
 #pragma unroll
-            for (int c = 0; c < kAStages; ++c) copy_a(c, c);
+            for (int c = 0; c < kAStages && c < NCH; ++c) copy_a(c, c);
         }
         load_b((int64_t)gn * kRows);
         first = false;
