@@ -300,14 +300,15 @@ __device__ __forceinline__ float wave_sum_f32(float v)
 // changes (a frame of tokens shares one), so a row costs its own bytes and
 // three binary32 operations per element before the rounding.
 template <int CPL, int WPR, bool NT, bool AFFINE, bool QUANT>
-__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant_blocks(NormArgs p, int64_t rb)
+__global__ __launch_bounds__(WPR * kLanes) void k_norm_quant_blocks(NormArgs p, int64_t rb)
 {
-    static_assert(kWavesPerBlock % WPR == 0, "rows per workgroup");
-    __shared__ float ssum[kWavesPerBlock];
-    __shared__ uint32_t smax[kWavesPerBlock];
+    // one group of WPR waves (one row at a time) per workgroup: the barriers that
+    // combine a row's partial sums hold up only the waves of that row
+    __shared__ float ssum[WPR];
+    __shared__ uint32_t smax[WPR];
     const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int part = wave % WPR;
-    const int64_t gid = (int64_t)blockIdx.x * (kWavesPerBlock / WPR) + wave / WPR;
+    const int64_t gid = (int64_t)blockIdx.x;
     const int64_t row0 = gid * rb;
     const int64_t row_end = min(p.M, row0 + rb);
     const int nch = (int)(p.K >> 3);
@@ -394,9 +395,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant_blocks(N
         if (WPR > 1) {
             if (lane == 0) ssum[wave] = ss;
             __syncthreads();
-            ss = ssum[(wave / WPR) * WPR];
+            ss = ssum[0];
 #pragma unroll
-            for (int w = 1; w < WPR; ++w) ss += ssum[(wave / WPR) * WPR + w];
+            for (int w = 1; w < WPR; ++w) ss += ssum[w];
         }
         const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
         uint32_t m2 = 0;
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_norm_quant_blocks(N
             if (lane == 0) smax[wave] = mbits;
             __syncthreads();
 #pragma unroll
-            for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[(wave / WPR) * WPR + w]);
+            for (int w = 0; w < WPR; ++w) mbits = max(mbits, smax[w]);
         }
         const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
         if (valid && part == 0 && lane == 0) p.y_scale[row] = scale;
@@ -654,17 +655,18 @@ extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K,
 
 namespace vdn {
 namespace {
-// k_norm_quant_blocks: WPR waves per row, rows in blocks of rb per wave group,
-// three workgroups per CU; false when no instantiated chunk count covers the row.
+// k_norm_quant_blocks: WPR waves per row and workgroup, rows in blocks of rb per
+// workgroup, kNormWavesPerCU waves per CU; false when no instantiated chunk count
+// covers the row.
+constexpr int kNormWavesPerCU = 12;
 template <int WPR, bool QUANT>
 bool launch_norm_blocks(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStream_t st)
 {
     const bool nt = p.normed && M * nch * 16 >= kNtStoreBytes;   // the normed bf16 output
     const int64_t per = (nch + WPR * kLanes - 1) / (WPR * kLanes);
-    const int64_t groups_per_wg = kWavesPerBlock / WPR;
-    const int64_t wgs = min((int64_t)cus * 3, (M + groups_per_wg - 1) / groups_per_wg);
-    const int64_t rb = (M + wgs * groups_per_wg - 1) / (wgs * groups_per_wg);
-    const dim3 grid((unsigned)((M + rb * groups_per_wg - 1) / (rb * groups_per_wg))), block(kWavesPerBlock * kLanes);
+    const int64_t wgs = min((int64_t)cus * (kNormWavesPerCU / WPR), M);
+    const int64_t rb = (M + wgs - 1) / wgs;
+    const dim3 grid((unsigned)((M + rb - 1) / rb)), block(WPR * kLanes);
     const bool affine = p.mod_scale != nullptr;
 #define VDN_LAUNCH(n, NT_, AF_) hipLaunchKernelGGL((k_norm_quant_blocks<n, WPR, NT_, AF_, QUANT>), grid, block, 0, st, p, rb)
 #define VDN_CASE(n)                                                          \
