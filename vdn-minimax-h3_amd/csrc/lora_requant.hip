@@ -473,7 +473,8 @@ struct RowArgs {
     float* w_scale;
     uint16_t* w_merged;  // MERGED only: rows ldw apart, 16-byte aligned
     int nch;             // ceil(K / 256)
-    int groups;          // ceil(N / 32)
+    int rows_pg;         // rows of W per group (<= 32; fewer so that the groups fill every CU)
+    int groups;          // ceil(N / rows_pg)
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -481,21 +482,21 @@ typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // One wave-wide global -> LDS copy of 16 bytes per lane: lane L's bytes at
-// buffer offset voff land at LDS byte lds + 16 L. Inline assembly, so that the
-// compiler does not make every later LDS read wait for it; the kernel waits on
-// vmcnt itself. M0 carries the LDS address (restored afterwards); s_nop covers
-// the M0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff)
+// buffer offset voff + soff (soff wave-uniform) land at LDS byte lds + 16 L.
+// Inline assembly, so that the compiler does not make every later LDS read wait
+// for it; the kernel waits on vmcnt itself. M0 carries the LDS address (restored
+// afterwards); s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff)
 {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(rsrc)
+        : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
         : "memory");
 }
 
@@ -562,22 +563,24 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     constexpr int kAStage = RP * kRowB;
     constexpr int kWCopies = kWStage / 1024 / rows::kWaves;  // 1 KiB W copies per wave per chunk (2)
     constexpr int kACopies = kAStage / 1024 / rows::kWaves;  // 1 KiB A copies per wave per chunk (RP / 16)
+    static_assert(kACopies + kWCopies <= 8, "a chunk's copies are spread over the eight words of a merge");
     constexpr int kWArea = kWStages * kWStage;
     constexpr int kAArea = kAStages * kAStage;
-    // The codes leave in parts of kPart chunks, staged by rows in the A area (rows
-    // padded by 16 bytes: the 16 rows one 16-byte write of a quarter-wave covers fall
-    // on 16 different bank quads); the last KiB of the A area holds the row maxima.
+    // The codes leave in parts of kPartC chunks (kPartC x 256 bytes of every row),
+    // staged by rows in the A area in two alternating buffers (rows padded by 16
+    // bytes: the 16 rows one 16-byte write of a quarter-wave covers fall on 16
+    // different bank quads); the last KiB of the A area holds the row maxima.
     constexpr int kRedOff = kWArea + kAArea - 1024;
-    constexpr int kPartMax = ((kAArea - 1024) / kRows - 16) / kChunk;
-    constexpr int kPart = kPartMax < NCH ? kPartMax : NCH;
-    constexpr int kParts = (NCH + kPart - 1) / kPart;
-    constexpr int kCRow = kPart * kChunk + 16;
-    static_assert(kPart >= 1 && kRows * kCRow <= kAArea - 1024, "codes staging exceeds the A area");
-    // 16-byte code stores per wave over all parts (rows wave + 8 i, 1 KiB pieces)
-    constexpr int kStorePieces = (kPart * kChunk + 1023) / 1024;
-    constexpr int kLastPart = NCH - (kParts - 1) * kPart;
-    constexpr int kLastPieces = (kLastPart * kChunk + 1023) / 1024;
-    constexpr int kStores = (kRows / rows::kWaves) * ((kParts - 1) * kStorePieces + kLastPieces) + (MERGED ? 2 * NCH : 0);
+    constexpr int kPartC = (2 * kRows * (4 * kChunk + 16) <= kAArea - 1024) ? 4
+                           : (2 * kRows * (2 * kChunk + 16) <= kAArea - 1024) ? 2 : 1;
+    constexpr int kParts = NCH / kPartC;
+    constexpr int kCRow = kPartC * kChunk + 16;
+    constexpr int kCBuf = kRows * kCRow;
+    static_assert(NCH % kPartC == 0 && 2 * kCBuf <= kAArea - 1024, "codes staging exceeds the A area");
+    // One 1 KiB store covers kRowsPerStore rows of a part; a wave stores kPartC of them
+    // per part, one while each chunk of the next part is formed.
+    constexpr int kRowsPerStore = 1024 / (kPartC * kChunk);
+    static_assert(kRows / kRowsPerStore == kPartC * rows::kWaves, "one store per wave and chunk");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kWArea + kAArea];
     uint32_t* const red = reinterpret_cast<uint32_t*>(smem + kRedOff);
 
@@ -585,6 +588,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nl = lane & 31, h = lane >> 5;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    const int64_t rpg = p.rows_pg;   // rows of a group (rows past it read as zeros, store nothing)
 
     // Copy i of a wave's W share moves rows 2 d and 2 d + 1 (d = 2 wave + i) of a chunk; lane L
     // fills row 2 d + L / 32, 16-byte piece L % 32, which holds the row's logical
@@ -592,38 +596,40 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     // fall on 16 different bank quads. Copy i of its A share moves rank rows 2 d and
     // 2 d + 1 (d = kACopies wave + i) of a slice, piece (L % 32) ^ (4 (row % 4)): the
     // four rank rows of one transposing read sit in four different 64-byte windows.
-    // (The lane-dependent offsets are formed where they are used, from opaque
-    // copies: kept for every copy they would hold registers throughout.)
+    // The row of copy i is 2 d + h with 2 d even, so the piece a lane fetches is
+    // ((L % 32) ^ h) ^ ((2 d) % 16) for W and ((L % 32) ^ 4 h) ^ 4 ((2 d) % 4) for A:
+    // a lane part held in registers (h rows down, that piece), xor'ed with a
+    // per-copy constant, and a uniform part (rows 2 d, the chunk) carried by the
+    // instruction's scalar offset.
     const i32x4_t arsrc = rsrc_words(p.a, p.rank * p.K * 2);
-    // (The row of copy i is 2 d + h with 2 d even, so its low bits are those of 2 d
-    // or'ed with h: the lane-dependent part of every offset is h times a row plus
-    // a 16-byte piece, the rest is uniform.)
     const uint32_t ldw2 = (uint32_t)(p.ldw * 2), k2 = (uint32_t)(p.K * 2);
+    const uint32_t w_lrow = (uint32_t)h * ldw2, w_lpc = (uint32_t)((nl ^ h) << 4);
+    const uint32_t a_lrow = (uint32_t)h * k2, a_lpc = (uint32_t)((nl ^ (4 * h)) << 4);
+    auto copy_w1 = [&](i32x4_t wrs, int c, int st, int i) {
+        const int d = kWCopies * wave + i;
+        uint32_t so = (uint32_t)(2 * d) * ldw2;
+        asm volatile("" : "+s"(so));   // the chunk's part added here, not kept per chunk
+        copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + d * 1024),
+                      (w_lpc ^ (uint32_t)(((2 * d) & 15) << 4)) + w_lrow, so + (uint32_t)(c * kRowB));
+    };
+    auto copy_a1 = [&](int c, int st, int i) {
+        const int d = kACopies * wave + i;
+        uint32_t so = (uint32_t)(2 * d) * k2;
+        asm volatile("" : "+s"(so));
+        copy16_to_lds(arsrc, lds_base + (uint32_t)(kWArea + st * kAStage + d * 1024),
+                      (a_lpc ^ (uint32_t)(((2 * d) & 3) << 6)) + a_lrow, so + (uint32_t)(c * kRowB));
+    };
     auto copy_w = [&](i32x4_t wrs, int c, int st) {
 #pragma unroll
-        for (int i = 0; i < kWCopies; ++i) {
-            int l = lane;
-            asm volatile("" : "+v"(l));
-            const int d = kWCopies * wave + i, hh = l >> 5;
-            const int lc = (l & 31) ^ (((2 * d) & 15) | hh);
-            copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + d * 1024),
-                          (uint32_t)hh * ldw2 + (uint32_t)(lc << 4) + (uint32_t)(2 * d) * ldw2 + (uint32_t)(c * kRowB));
-        }
+        for (int i = 0; i < kWCopies; ++i) copy_w1(wrs, c, st, i);
     };
     auto copy_a = [&](int c, int st) {
 #pragma unroll
-        for (int i = 0; i < kACopies; ++i) {
-            int l = lane;
-            asm volatile("" : "+v"(l));
-            const int d = kACopies * wave + i, hh = l >> 5;
-            const int lc = (l & 31) ^ (4 * (((2 * d) & 3) | hh));
-            copy16_to_lds(arsrc, lds_base + (uint32_t)(kWArea + st * kAStage + d * 1024),
-                          (uint32_t)hh * k2 + (uint32_t)(lc << 4) + (uint32_t)(2 * d) * k2 + (uint32_t)(c * kRowB));
-        }
+        for (int i = 0; i < kACopies; ++i) copy_a1(c, st, i);
     };
     // W descriptor of a group (empty past the last group: reads zeros, touches no memory)
     auto w_rsrc = [&](int64_t n0) {
-        const int64_t rows = n0 < p.N ? min(p.N - n0, (int64_t)kRows) : 0;
+        const int64_t rows = n0 < p.N ? min(p.N - n0, rpg) : 0;
         return rsrc_words(p.w + n0 * p.ldw, rows * p.ldw * 2);
     };
     // Transposing reads: lane (group G = lane / 16, j = (lane / 4) % 4, q = lane % 4)
@@ -652,7 +658,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     // raw 16-byte loads are masked where they are first used.
     bf16x8_t braw[kSteps];
     auto load_b = [&](int64_t n0) {
-        const int64_t rows = n0 < p.N ? min(p.N - n0, (int64_t)kRows) : 0;
+        const int64_t rows = n0 < p.N ? min(p.N - n0, rpg) : 0;
         const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(p.b + n0 * p.rank), 0, (int)(rows * p.rank * 2), 0x00020000);
 #pragma unroll
@@ -664,9 +670,9 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     int g = blockIdx.x;
     if (g >= p.groups) return;
     // Prologue of the first group: B, then W0 A0 W1 A1 W2 A2 W3.
-    load_b((int64_t)g * kRows);
+    load_b((int64_t)g * rpg);
     {
-        const i32x4_t wrs = w_rsrc((int64_t)g * kRows);
+        const i32x4_t wrs = w_rsrc((int64_t)g * rpg);
 #pragma unroll
         for (int c = 0; c < kWStages && c < NCH; ++c) {
             copy_w(wrs, c, c);
@@ -677,17 +683,20 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     uint32_t wr[NCH][8];
     bool first = true;
     for (; g < p.groups; g += gridDim.x) {
-        const int64_t n0 = (int64_t)g * kRows;
-        const int64_t rows = min(p.N - n0, (int64_t)kRows);
+        const int64_t n0 = (int64_t)g * rpg;
+        const int64_t rows = min(p.N - n0, rpg);
         const i32x4_t wrs = w_rsrc(n0);
         bf16x8_t bop[kSteps];
 
         // Merge: W' = bf16(W + bf16(scale * B A)) per chunk, into wr[c]; mx keeps the
-        // packed bf16 magnitude maximum of the valid columns. Software-pipelined by one
+        // magnitude maximum of the valid columns' binary32 sums before their rounding
+        // (rounding to nearest is monotone and symmetric, so the row maximum of |W'| is
+        // that maximum rounded; v_maximum3_f32 takes two magnitudes an instruction and
+        // propagates NaN). Software-pipelined by one
         // chunk: chunk c's LDS reads go out, then chunk c - 1's VALU work (its MFMAs
         // have had a chunk's time to finish) hides their latency, then chunk c's MFMAs
         // run while the next chunk waits for its data.
-        uint32_t mx = 0u;
+        float mx = 0.0f;
         f32x16_t acc;   // chunk c's sums, read by back(c) before mfmas(c + 1) rewrites them
         auto front = [&](int c) {
             if (c == 0) {
@@ -725,25 +734,37 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             for (int s = 0; s < kSteps; ++s) a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[s], bop[s], a, 0, 0, 0);
             acc = a;
         };
-        auto copies = [&](int c) {
-            // Every wave is past chunk c - 1, so its stages can take chunk
-            // c + kWStages - 1 (W) and slice c + kAStages - 1 (A).
-            if (c >= 1 && c + kAStages - 1 < NCH) copy_a(c + kAStages - 1, (c + kAStages - 1) % kAStages);
-            if (c >= 1 && c + kWStages - 1 < NCH) copy_w(wrs, c + kWStages - 1, (c + kWStages - 1) % kWStages);
+        // Copy j (0 .. kACopies + kWCopies - 1) of chunk c: every wave is past chunk
+        // c - 1, so its stages can take slice c + kAStages - 1 (A, copies j < kACopies)
+        // and chunk c + kWStages - 1 (W, the others), requested in that order.
+        auto copy_j = [&](int c, int j) {
+            if (j < kACopies) {
+                if (c >= 1 && c + kAStages - 1 < NCH) copy_a1(c + kAStages - 1, (c + kAStages - 1) % kAStages, j);
+            } else if (j < kACopies + kWCopies) {
+                if (c >= 1 && c + kWStages - 1 < NCH) copy_w1(wrs, c + kWStages - 1, (c + kWStages - 1) % kWStages, j - kACopies);
+            }
         };
-        auto back = [&](int c) {
+        // back(c, cn): chunk c's merge, with chunk cn's copies spread over it (one after
+        // each of the first words), so the copy path works while the VALU does.
+        auto back = [&](int c, int cn) {
             const f32x16_t& a = acc;
-            uint32_t gm = 0u;
+            float gm = 0.0f;
 #pragma unroll
             for (int d = 0; d < 8; ++d) {
+                if (cn >= 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    copy_j(cn, d);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 uint32_t dl = pack_bf16x2(a[2 * d] * p.lora_scale, a[2 * d + 1] * p.lora_scale);
                 asm volatile("" : "+v"(dl));
-                uint32_t m = pack_bf16x2(bf16_lo(wr[c][d]) + bf16_lo(dl), bf16_hi(wr[c][d]) + bf16_hi(dl));
+                const float lo = bf16_lo(wr[c][d]) + bf16_lo(dl), hi = bf16_hi(wr[c][d]) + bf16_hi(dl);
+                uint32_t m = pack_bf16x2(lo, hi);
                 asm volatile("" : "+v"(m));
                 wr[c][d] = m;
-                gm = absmax_bf16x2(gm, m);
+                gm = __builtin_elementwise_maximum(gm, __builtin_elementwise_maximum(__builtin_fabsf(lo), __builtin_fabsf(hi)));
             }
-            mx = col_in(c) ? absmax_bf16x2(mx, gm) : mx;
+            mx = col_in(c) ? __builtin_elementwise_maximum(mx, gm) : mx;
         };
         static_for<NCH>([&](auto ic) {
             constexpr int c = decltype(ic)::value;
@@ -760,20 +781,18 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             reads_w(c);
             reads_a(c, aop, 0, kSteps / 2);
             __builtin_amdgcn_sched_barrier(0);
-            if (c >= 1) back(c - 1);
+            if (c >= 1) back(c - 1, c);
             __builtin_amdgcn_sched_barrier(0);
             reads_a(c, aop, kSteps / 2, kSteps);
             mfmas(c, aop);
             __builtin_amdgcn_sched_barrier(0);
-            copies(c);
-            __builtin_amdgcn_sched_barrier(0);
         });
-        back(NCH - 1);
+        back(NCH - 1, -1);
 
         // Row maxima: the two halves of each lane's words, the two lanes of a row,
         // then the eight waves through LDS (in the last KiB of the A area: written
         // once every wave is done with the last chunk).
-        uint32_t m16 = max(mx & 0xffffu, mx >> 16);
+        uint32_t m16 = pack_bf16x2(mx, 0.0f) & 0x7fffu;   // bf16 magnitude bits (NaN above inf)
         m16 = max(m16, (uint32_t)__shfl_xor((int)m16, 32, 64));
         rows_sync<63>();
         if (h == 0) red[wave * kRows + nl] = m16;
@@ -797,16 +816,15 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         // its last chunk), then the codes, part by part.
         const int gn = g + (int)gridDim.x;
         const bool more = gn < p.groups;
-        const i32x4_t nrs = w_rsrc((int64_t)gn * kRows);
+        const i32x4_t nrs = w_rsrc((int64_t)gn * rpg);
 #pragma unroll
         for (int c = 0; c < kWStages && c < NCH; ++c) copy_w(nrs, c, c);
         const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(p.wq + n0 * p.ldq), 0, (int)(rows * p.ldq), 0x00020000);
         const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(MERGED ? p.w_merged + n0 * p.ldw : nullptr), 0, MERGED ? (int)(rows * p.ldw * 2) : 0, 0x00020000);
-        uint8_t* const cst = smem + kWArea;
         // (one uniform branch per chunk around the quotients only)
-        auto codes_chunk = [&](int c, int c0) {
+        auto codes_chunk = [&](int c, int c0, uint8_t* cst) {
             uint32_t q[4];
             if (exact) {
 #pragma unroll
@@ -830,41 +848,48 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             }
             __builtin_amdgcn_sched_barrier(0);
         };
-        // Rows wave + 8 i of a part, 1 KiB (64 lanes x 16 bytes) per store; columns past
-        // K and rows past N go out of range.
-        auto store_part = [&](int c0, int nc) {
-            const int bytes = nc * kChunk;
+        // Store j of a wave in a part: rows kRowsPerStore (kPartC wave + j) .., lane L at
+        // row + L / (16 kPartC), bytes 16 (L % (16 kPartC)) of the part's kPartC x 256.
+        // Columns past K and rows past the group go out of range.
+        constexpr int kLanesPerRow = 16 * kPartC;
+        const int srow = lane / kLanesPerRow, sbyte = 16 * (lane % kLanesPerRow);
+        uint4 pend[kPartC];
+        auto read_part = [&](const uint8_t* cst) {
 #pragma unroll
-            for (int i = 0; i < kRows / rows::kWaves; ++i) {
-                const int row = wave + rows::kWaves * i;
-#pragma unroll
-                for (int j = 0; j < kStorePieces; ++j) {
-                    const int b = 1024 * j + 16 * lane;
-                    if (1024 * j < bytes) {
-                        const uint4 v = *reinterpret_cast<const uint4*>(cst + row * kCRow + min(b, bytes - 16));
-                        const int64_t col = (int64_t)c0 * kChunk + b;
-                        const uint32_t off = (b < bytes && col < p.K) ? (uint32_t)(row * p.ldq + b) : kDropped;
-                        store16_settled(__builtin_bit_cast(i32x4_t, v), qr, off, c0 * kChunk);
-                    }
-                }
+            for (int j = 0; j < kPartC; ++j) {
+                const int row = kRowsPerStore * (kPartC * wave + j) + srow;
+                pend[j] = *reinterpret_cast<const uint4*>(cst + row * kCRow + sbyte);
             }
         };
+        auto store_piece = [&](int c0, int j) {
+            const int row = kRowsPerStore * (kPartC * wave + j) + srow;
+            const uint32_t off = ((int64_t)c0 * kChunk + sbyte < p.K) ? (uint32_t)(row * p.ldq + sbyte) : kDropped;
+            store16_settled(__builtin_bit_cast(i32x4_t, pend[j]), qr, off, c0 * kChunk);
+        };
+        // Part q's codes go to buffer q % 2 while part q - 1's pieces are stored; then
+        // (all of part q in LDS, every wave past its reads of part q - 1) part q's pieces
+        // are read. The buffer part q + 1 overwrites is part q - 1's, read before that.
+        static_for<kParts>([&](auto iq) {
+            constexpr int q = decltype(iq)::value;
+            uint8_t* const cst = smem + kWArea + (q % 2) * kCBuf;
 #pragma unroll
-        for (int part = 0; part < kParts; ++part) {
-            const int c0 = part * kPart;
-            const int nc = part + 1 < kParts ? kPart : kLastPart;
+            for (int j = 0; j < kPartC; ++j) {
+                codes_chunk(q * kPartC + j, q * kPartC, cst);
+                if (q >= 1) store_piece((q - 1) * kPartC, j);
+            }
+            rows_sync<63>();
+            read_part(cst);
+        });
+        // every wave's reads of the last part are done before the A stages are refilled
+        rows_sync<63>();
 #pragma unroll
-            for (int c = c0; c < c0 + nc; ++c) codes_chunk(c, c0);
-            rows_sync<63>();
-            store_part(c0, nc);
-            rows_sync<63>();
-        }
+        for (int j = 0; j < kPartC; ++j) store_piece((kParts - 1) * kPartC, j);
         // The next group's first A slices (the A area is free again) and B rows.
         if (more) {
 #pragma unroll
             for (int c = 0; c < kAStages && c < NCH; ++c) copy_a(c, c);
         }
-        load_b((int64_t)gn * kRows);
+        load_b((int64_t)gn * rpg);
         first = false;
     }
     // No copy may still be writing LDS when the workgroup ends.
@@ -955,12 +980,14 @@ int launch_lora_requant(const uint16_t* w, int64_t N, int64_t K, int64_t ldw, co
                           (!w_merged || aligned(w_merged, 16)) && (int64_t)rows::kRows * ldw * 2 <= 0x7fffffffLL &&
                           (int64_t)rows::kRows * ldq <= 0x7fffffffLL && rank * K * 2 <= 0x7fffffffLL;
     if (one_pass) {
+        // persistent grid, one workgroup per CU: as many rounds of groups as 32-row
+        // groups would need, then the rows spread evenly over rounds x CUs groups
+        // ([15360, *] on 256 CUs: 512 groups of 30 rows, two per workgroup)
+        const int64_t rounds = (N + (int64_t)rows::kRows * cus - 1) / ((int64_t)rows::kRows * cus);
+        const int rows_pg = (int)((N + rounds * cus - 1) / (rounds * cus));
         RowArgs r{w, N, K, ldw, a, b, rank, lora_scale, wq, ldq, w_scale, w_merged,
-                  (int)((K + rows::kChunk - 1) / rows::kChunk), (int)((N + rows::kRows - 1) / rows::kRows)};
-        // persistent grid: as many rounds of groups as the CUs need, the groups spread
-        // evenly over the workgroups (480 groups on 256 CUs: 240 workgroups of two)
-        const int64_t rounds = (r.groups + cus - 1) / cus;
-        const dim3 grid((unsigned)((r.groups + rounds - 1) / rounds)), block(rows::kThreads);
+                  (int)((K + rows::kChunk - 1) / rows::kChunk), rows_pg, (int)((N + rows_pg - 1) / rows_pg)};
+        const dim3 grid((unsigned)min((int64_t)r.groups, (int64_t)cus)), block(rows::kThreads);
         // chunk-count instances: 8 (K <= 2048), 16 (K <= 4096), 20 (K <= 5120); chunks past
         // K read nothing and store nothing
 #define VDN_LORA_ROWS(R, C)                                                                            \
