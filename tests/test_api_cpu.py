@@ -152,3 +152,24 @@ def test_load_external_lora_alpha(tmp_path):
     save_file(t, str(p))
     assert load_external_lora(str(p))[1] == 1.0
     assert load_external_lora(str(p), alpha=16)[1] == 2.0
+
+
+def test_swiglu_one_rounding_against_float64():
+    """The bf16 feed-forward's SwiGLU rounds a * silu(gate) once, as the reference's
+    compiled body (fused_block.py:88); the eager body rounds silu first. Against
+    a * g / (1 + exp(-g)) in float64 rounded once: within one bf16 step everywhere and
+    identical almost everywhere, while the eager body differs far more often."""
+    import numpy as np
+    from vdn_fp8 import fused_block as FB
+    g = torch.Generator().manual_seed(11)
+    h = (torch.randn(256, 2 * 512, generator=g) * torch.logspace(-2, 1, 2 * 512)).to(torch.bfloat16)
+    got = FB._swiglu_one_rounding(h).float().numpy().astype(np.float64)
+    eager = FB._swiglu_ref(h).float().numpy().astype(np.float64)
+    a, gate = (t.float().numpy().astype(np.float64) for t in h.chunk(2, dim=-1))
+    exact = a * gate / (1.0 + np.exp(-gate))
+    want = torch.from_numpy(exact).to(torch.bfloat16).float().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(got - want) <= ulp)
+    same, same_eager = np.mean(got == want), np.mean(eager == want)
+    assert same >= 0.995, same
+    assert same_eager < same, (same_eager, same)

@@ -192,6 +192,26 @@ def test_fast_ff_forward_matches_oracle_chain(device):
     assert np.mean(got == want) >= 0.75
 
 
+def test_fast_ff_forward_bf16_rounds_once(device):
+    """A feed-forward whose linears stay bf16: the projection, the SwiGLU rounded once
+    (the reference's compiled body, fused_block.py:88; its numerics are pinned against
+    float64 in the CPU tests), then the down projection."""
+    C, I = 256, 128
+    g = torch.Generator().manual_seed(4)
+    proj = nn.Linear(C, 2 * I, dtype=torch.bfloat16).to(device)
+    down = nn.Linear(I, C, dtype=torch.bfloat16).to(device)
+    ff = _FF(proj, down)
+    x = torch.randn(2, 20, C, generator=g).to(torch.bfloat16).to(device)
+    with torch.no_grad():
+        got = FB.fast_ff_forward(ff, x)
+        want = down(FB._swiglu_one_rounding(proj(x.reshape(-1, C)))).reshape(2, 20, C)
+        eager = down(FB._swiglu_ref(proj(x.reshape(-1, C)))).reshape(2, 20, C)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    print(f"bf16 feed-forward: {torch.mean((got != eager).float()).item():.3f} of outputs differ from the "
+          f"eager SwiGLU's", flush=True)
+
+
 def test_fast_block_forward_bf16_ff(device):
     """A block whose feed-forward stays bf16 (no Fp8Linear): pre, the module, post."""
     M, C, I, T = 48, 512, 256, 2

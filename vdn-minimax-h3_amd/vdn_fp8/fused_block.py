@@ -19,7 +19,8 @@ stretch, one rounding at its store (the reference's own caveat: not bitwise with
 bodies, which round after every op).
 
 The eager bodies `_pre_ref`, `_post_ref`, `_swiglu_ref` are kept with the reference's names
-and meaning for callers that import them; nothing on the fast path uses them.
+and meaning for callers that import them; nothing on the fast path uses them (a bf16
+feed-forward uses `_swiglu_one_rounding`, the compiled body's arithmetic).
 """
 import torch
 import torch.nn.functional as F
@@ -48,6 +49,14 @@ def _swiglu_ref(h):
     """SwiGLU after its projection: a * silu(gate), (a, gate) = h.chunk(2) (eager)."""
     a, gate = h.chunk(2, dim=-1)
     return a * F.silu(gate)
+
+
+def _swiglu_one_rounding(h):
+    """The SwiGLU body as the reference's compiled region computes it
+    (`_compiled("swiglu", _swiglu_ref)`, fused_block.py:88): a * silu(gate) in binary32,
+    rounded once to h's dtype (eager rounds silu first, then the product)."""
+    a, gate = h.chunk(2, dim=-1)
+    return (a.float() * F.silu(gate.float())).to(h.dtype)
 
 
 # --------------------------------------------------------------------------------------
@@ -159,14 +168,15 @@ def fast_ff_forward(self, hidden_states):
     """Drop-in for FeedForward.forward ([SwiGLU, Dropout, Linear]) at inference
     (fused_block.py:73-90): the projection GEMM, then -- with an fp8 down projection --
     SwiGLU fused with the down projection's quantization (the bf16 activation is never
-    written) and the down GEMM; otherwise the eager activation and the down layer."""
+    written) and the down GEMM; otherwise the activation with one rounding, as the
+    reference's compiled body, and the down layer."""
     swiglu, _, down = self.net
     shape = hidden_states.shape
     h = swiglu.proj(hidden_states.reshape(-1, shape[-1]))
     if isinstance(down, Fp8Linear):
         out = down.forward_quantized(*swiglu_quantize_activation(h), out_dtype=h.dtype)
     else:
-        out = down(_swiglu_ref(h))
+        out = down(_swiglu_one_rounding(h))
     return out.reshape(*shape[:-1], -1)
 
 
