@@ -416,64 +416,106 @@ void k_gemm_fp8(GemmArgs p)
         const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(p.out + m0 * p.ldo), 0, (int)min(min(p.M - m0, (int64_t)BM) * p.ldo * 2, (int64_t)0x7fffffff), kRsrcWord3);
         const uint32_t ldo2 = (uint32_t)p.ldo * 2;
+        // Slabs in order (th, u) = (1, 3), (1, 2), .. (0, 0). A column half's per-column
+        // vectors (w_scale, bias and a broadcast gate row, unpacked to binary32) are read
+        // from LDS once and held in registers across its four slabs -- the K loop's
+        // fragment registers are free here. On the fast path the stores trail by one
+        // slab: the previous slab's rows are read back from the staging before this
+        // slab's values overwrite it (a wave's LDS operations run in order), so its
+        // computation hides that read's latency.
+        const bool has_bias = p.bias != nullptr;
+        float hsw[2][4][4], hb[2][4][4], hg[2][4][4];
+        auto hoist = [&](int th) {
 #pragma unroll
-        for (int uu = 0; uu < 4; ++uu) {
-            const int u = 3 - uu;
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int nl = wn * 128 + 32 * (2 * th + t2) + 8 * q + 4 * fh;
+                    const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
+                    hsw[t2][q][0] = sw.x; hsw[t2][q][1] = sw.y; hsw[t2][q][2] = sw.z; hsw[t2][q][3] = sw.w;
+                    if (has_bias) {
+                        const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
+                        hb[t2][q][0] = bf16_lo(b.x); hb[t2][q][1] = bf16_hi(b.x);
+                        hb[t2][q][2] = bf16_lo(b.y); hb[t2][q][3] = bf16_hi(b.y);
+                    }
+                    if (EPI == VDN_FP8_EPI_GATE && FAST) {
+                        const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
+                        hg[t2][q][0] = bf16_lo(gv.x); hg[t2][q][1] = bf16_hi(gv.x);
+                        hg[t2][q][2] = bf16_lo(gv.y); hg[t2][q][3] = bf16_hi(gv.y);
+                    }
+                }
+        };
+        // bf16 GEMM output, then the bf16 bias add: each rounding done two values per
+        // conversion, the second one's pairs being the stored words (opaque, so the
+        // compiler keeps the pairs); one uniform branch per slab
+        auto compute = [&](int th, int u, auto with_bias) {
             const float sxm = s_sx[wm * 128 + 32 * u + frow];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int th = 1 - tt;
+            for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-                for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int t = 2 * th + t2;
-                        const int nl = wn * 128 + 32 * t + 8 * q + 4 * fh;
-                        const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
-                        const float swv[4] = {sw.x, sw.y, sw.z, sw.w};
-                        // bf16 GEMM output, then the bf16 bias add: each rounding done
-                        // two values per conversion, the second one's pairs being the
-                        // stored words (opaque, so the compiler keeps the pairs)
-                        uint32_t r01 = pack_bf16x2(acc[t][u][4 * q] * (sxm * swv[0]), acc[t][u][4 * q + 1] * (sxm * swv[1]));
-                        uint32_t r23 = pack_bf16x2(acc[t][u][4 * q + 2] * (sxm * swv[2]), acc[t][u][4 * q + 3] * (sxm * swv[3]));
+                for (int q = 0; q < 4; ++q) {
+                    const int t = 2 * th + t2;
+                    const float* sw = hsw[t2][q];
+                    uint32_t r01 = pack_bf16x2(acc[t][u][4 * q] * (sxm * sw[0]), acc[t][u][4 * q + 1] * (sxm * sw[1]));
+                    uint32_t r23 = pack_bf16x2(acc[t][u][4 * q + 2] * (sxm * sw[2]), acc[t][u][4 * q + 3] * (sxm * sw[3]));
+                    asm volatile("" : "+v"(r01), "+v"(r23));
+                    if (decltype(with_bias)::value) {
+                        const float* bb = hb[t2][q];
+                        r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
+                        r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
                         asm volatile("" : "+v"(r01), "+v"(r23));
-                        if (p.bias) {
-                            const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
-                            r01 = pack_bf16x2(bf16_lo(r01) + bf16_lo(b.x), bf16_hi(r01) + bf16_hi(b.x));
-                            r23 = pack_bf16x2(bf16_lo(r23) + bf16_lo(b.y), bf16_hi(r23) + bf16_hi(b.y));
-                            asm volatile("" : "+v"(r01), "+v"(r23));
-                        }
-                        if (EPI == VDN_FP8_EPI_GELU_TANH) {
-                            r01 = pack_bf16x2(gelu_tanh(bf16_lo(r01)), gelu_tanh(bf16_hi(r01)));
-                            r23 = pack_bf16x2(gelu_tanh(bf16_lo(r23)), gelu_tanh(bf16_hi(r23)));
-                        }
-                        if (EPI == VDN_FP8_EPI_GATE && FAST) {   // broadcast gate row, no residual
-                            const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
-                            r01 = pack_bf16x2(bf16_lo(r01) * bf16_lo(gv.x), bf16_hi(r01) * bf16_hi(gv.x));
-                            r23 = pack_bf16x2(bf16_lo(r23) * bf16_lo(gv.y), bf16_hi(r23) * bf16_hi(gv.y));
-                        }
-                        *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
                     }
-                // these accumulators start the next tile from zero
-                acc[2 * th][u] = f32x16_t{};
-                acc[2 * th + 1][u] = f32x16_t{};
+                    if (EPI == VDN_FP8_EPI_GELU_TANH) {
+                        r01 = pack_bf16x2(gelu_tanh(bf16_lo(r01)), gelu_tanh(bf16_hi(r01)));
+                        r23 = pack_bf16x2(gelu_tanh(bf16_lo(r23)), gelu_tanh(bf16_hi(r23)));
+                    }
+                    if (EPI == VDN_FP8_EPI_GATE && FAST) {   // broadcast gate row, no residual
+                        const float* gg = hg[t2][q];
+                        r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
+                        r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
+                    }
+                    *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
+                }
+            // these accumulators start the next tile from zero
+            acc[2 * th][u] = f32x16_t{};
+            acc[2 * th + 1][u] = f32x16_t{};
+        };
+        // fast path: the slab's rows 8 i + L/8 from the staging, then their stores (byte
+        // offset of the row, or out of range past N)
+        uint4 pv[4];
+        auto read_slab = [&]() {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[i] = *reinterpret_cast<const uint4*>(stg + (8 * i + rl) * kStgRow + (cc << 4));
+        };
+        auto store_slab = [&](int th, int u) {
+            const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
+            const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t off = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off, 0, kStoreNT);
+            }
+        };
+#pragma unroll
+        for (int sidx = 0; sidx < 8; ++sidx) {
+            const int th = 1 - sidx / 4, u = 3 - sidx % 4;
+            if (sidx % 4 == 0) hoist(th);
+            if (FAST && sidx > 0) read_slab();   // the previous slab, before this one overwrites it
+            if (has_bias) compute(th, u, std::true_type{});
+            else compute(th, u, std::false_type{});
+            if (FAST) {
+                if (sidx > 0) store_slab(1 - (sidx - 1) / 4, 3 - (sidx - 1) % 4);
+            } else {
                 const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
                 const bool full = n + 8 <= p.N;
-                // fast path: byte offset of row 8 i + L/8 of this slab, or out of range
-                const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 8 * i + rl;
                     uint4 v = *reinterpret_cast<const uint4*>(stg + r * kStgRow + (cc << 4));
-                    if (FAST) {
-                        const uint32_t off = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), orr, off, 0, kStoreNT);
-                        continue;
-                    }
                     const int ml = wm * 128 + 32 * u + r;
                     const int64_t m = m0 + ml;
                     if (m >= p.M || n >= p.N) continue;
-                    if (EPI == VDN_FP8_EPI_GATE && !FAST) {
+                    if (EPI == VDN_FP8_EPI_GATE) {
                         const int64_t gi = p.gate_index ? min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1) : 0;
                         const uint16_t* gp = p.gate + gi * p.ldgate + n;
                         uint4 g;
@@ -508,9 +550,13 @@ void k_gemm_fp8(GemmArgs p)
                     *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
                     if (full) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
                 }
-                // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
-                __builtin_amdgcn_sched_barrier(0);
             }
+            // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (FAST) {   // the last slab (th 0, u 0)
+            read_slab();
+            store_slab(0, 0);
         }
     };
 
