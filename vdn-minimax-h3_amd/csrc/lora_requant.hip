@@ -8,6 +8,12 @@
 // quantizes it in eager torch (fp8_linear.py:262-267): several full passes over
 // W plus the write-back of W'. Here W' is never stored unless asked for.
 //
+// Two kernels. k_lora_rows (further down; rank <= 64, K <= 5120, 16-byte rows)
+// reads W once: a workgroup holds a group of whole rows of W' in registers
+// until their maximum is known, then writes the codes. k_lora_stripes (first)
+// serves everything else -- ranks up to 128, longer rows, unaligned operands,
+// merge-only calls -- in two passes:
+//
 // Work split: the weight is cut into 256-column stripes and 64-row tiles. A
 // workgroup (four waves, 16 rows each) owns one stripe and walks a set of its
 // row tiles, so the stripe's slice of A is staged in LDS once per workgroup;
@@ -411,19 +417,21 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
 //
 // Both streams reach LDS by global -> LDS copies: W (from HBM) through four
 // 16 KiB stages, A (from L2) through three; every wave issues its share of both
-// (2 W and RP / 16 A copies of 1 KiB per chunk). A wave's memory counter orders
-// its operations as issued, so slice c of A is requested after chunk c of W and
-// before chunk c + 1: one exact wait for slice c then covers both, while W of
-// chunks c + 1 and c + 2 stays in flight (chunk c + 3 goes out after it), and
-// the merge of chunk c runs meanwhile. After the last chunk the row maxima meet
-// in LDS; the next group's first four W chunks are requested, and the codes
-// leave through LDS (the A stages' space) as whole 1 KiB row pieces, part by
-// part, while those chunks stream in. The grid is persistent, one workgroup
-// per CU.
+// (2 W and RP / 16 A copies of 1 KiB per chunk, spread over the previous
+// chunk's merge). A wave's memory counter orders its operations as issued, so
+// slice c of A is requested after chunk c of W and before chunk c + 1: one
+// exact wait for slice c then covers both, while W of chunks c + 1 and c + 2
+// stays in flight (chunk c + 3 goes out after it), and the merge of chunk c
+// runs meanwhile. After the last chunk the row maxima meet in LDS; the next
+// group's first four W chunks are requested, and the codes leave through LDS
+// (the A stages' space, two alternating buffers) as whole 1 KiB row pieces,
+// four chunks at a time, while those chunks stream in; then the next group's
+// first A slices and B rows. The grid is persistent, one workgroup per CU, the
+// rows spread evenly over its groups (up to 32 rows each).
 namespace rows {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kLanes;   // 512
-constexpr int kRows = 32;                   // rows of W per group
+constexpr int kRows = 32;                   // rows of W per group (at most)
 constexpr int kChunk = 256;                 // columns per chunk (32 per wave)
 constexpr int kMaxChunks = 20;              // K <= 5120
 constexpr int kWStages = 4;                 // W chunks in LDS (16 KiB each)
