@@ -89,7 +89,10 @@ def _check_lora(w, a, b, scale, device, max_mismatch=2e-3):
                                    # odd ranks (2-byte B rows), partial column stripes, one row,
                                    # partial row tiles
                                    (24, 2048, 5), (70, 1280, 33), (9, 272, 19), (130, 4112, 64),
-                                   (1, 5120, 64), (200, 768, 127)])
+                                   (1, 5120, 64), (200, 768, 127),
+                                   # one-pass row groups of 28 rows with a short last group, and
+                                   # two rounds of 18-row groups over uneven workgroups
+                                   (6999, 2048, 32), (9000, 1024, 64)])
 def test_requant_lora_shapes(device, N, K, r):
     print(f"lora requant N={N} K={K} r={r}", flush=True)
     rng = np.random.default_rng(N + K + r)
