@@ -298,9 +298,10 @@ __device__ __forceinline__ float wave_sum_f32(float v)
 // flight while the current one is computed. The per-column factors f and the
 // shift (binary32) stay in VGPRs and are formed again only when the table row
 // changes (a frame of tokens shares one), so a row costs its own bytes and
-// three binary32 operations per element before the rounding.
+// three binary32 operations per element before the rounding. The waves-per-EU
+// bound holds the kernel to 168 VGPRs, so three waves share each SIMD.
 template <int CPL, int WPR, bool NT, bool AFFINE, bool QUANT>
-__global__ __launch_bounds__(WPR * kLanes) void k_norm_quant_blocks(NormArgs p, int64_t rb)
+__global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CPL <= 5 ? 3 : 1))) void k_norm_quant_blocks(NormArgs p, int64_t rb)
 {
     // one group of WPR waves (one row at a time) per workgroup: the barriers that
     // combine a row's partial sums hold up only the waves of that row
@@ -400,7 +401,7 @@ __global__ __launch_bounds__(WPR * kLanes) void k_norm_quant_blocks(NormArgs p, 
             for (int w = 1; w < WPR; ++w) ss += ssum[w];
         }
         const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
-        uint32_t m2 = 0;
+        float mf = 0.0f;                             // row maximum of |n| (binary32)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
@@ -416,13 +417,12 @@ __global__ __launch_bounds__(WPR * kLanes) void k_norm_quant_blocks(NormArgs p, 
                     b *= f[c][2 * e + 1];
                 }
                 o[e] = pack_bf16x2(a, b);
+                // max(|a|, |b|, mf) in one v_maximum3_f32 (NaN propagates)
+                mf = __builtin_elementwise_maximum(
+                    mf, __builtin_elementwise_maximum(__builtin_fabsf(a), __builtin_fabsf(b)));
             }
             // chunks past K hold zeros (x = 0, f = 0, shift = 0): nothing to the maximum
             v[c] = make_uint4(o[0], o[1], o[2], o[3]);
-            m2 = absmax_bf16x2(m2, v[c].x);
-            m2 = absmax_bf16x2(m2, v[c].y);
-            m2 = absmax_bf16x2(m2, v[c].z);
-            m2 = absmax_bf16x2(m2, v[c].w);
         }
         const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)uniform((int64_t)(p.normed ? p.normed + (valid ? row : 0) * p.ldn : nullptr)), 0,
@@ -434,7 +434,9 @@ __global__ __launch_bounds__(WPR * kLanes) void k_norm_quant_blocks(NormArgs p, 
                                                        NT ? kBufferLoadOnce : 0);
             return;
         }
-        uint32_t mbits = wave_max_u32(max(m2 & 0xffffu, m2 >> 16));
+        // bf16 rounding is monotone and odd, so the bf16 of the binary32 maximum of |n|
+        // is the maximum of the rounded |n| quantize_rows takes (NaN stays NaN)
+        uint32_t mbits = wave_max_u32(pack_bf16x2(mf, 0.0f) & 0x7fffu);
         if (WPR > 1) {
             if (lane == 0) smax[wave] = mbits;
             __syncthreads();
