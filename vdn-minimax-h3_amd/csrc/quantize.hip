@@ -274,9 +274,16 @@ struct NormArgs {
 
 __device__ __forceinline__ float wave_sum_f32(float v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    // pairwise within the rows (both lanes of each exchange form the same sum), then
+    // (row 0 + row 1) + (row 2 + row 3), wave-uniform
+    v += __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v)));
+    const uint32_t u = __float_as_uint(v);
+    const float r0 = __uint_as_float(__builtin_amdgcn_readlane(u, 0)), r1 = __uint_as_float(__builtin_amdgcn_readlane(u, 16)),
+                r2 = __uint_as_float(__builtin_amdgcn_readlane(u, 32)), r3 = __uint_as_float(__builtin_amdgcn_readlane(u, 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // The block's pre-norm fused with the per-token quantization:

@@ -95,12 +95,27 @@ __device__ __forceinline__ uint32_t absmax_bf16x2(uint32_t acc, uint32_t w)
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
 }
 
-// Maximum over the 64 lanes of a wavefront.
+// Lane exchanges inside each row of 16 lanes (DPP, no LDS round trip): xor 1, xor 2,
+// the mirror within 8 lanes and the mirror within 16. After the four steps of a
+// reduction every lane of a row holds the row's result. The wavefront must be whole.
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xf, 0xf, false);
+}
+
+// Maximum over the 64 lanes of a wavefront, wave-uniform: four DPP steps within the
+// rows, then the four row maxima read into scalar registers.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
-    return v;
+    v = max(v, dpp_u32<kDppXor1>(v));
+    v = max(v, dpp_u32<kDppXor2>(v));
+    v = max(v, dpp_u32<kDppHalfMirror>(v));
+    v = max(v, dpp_u32<kDppMirror>(v));
+    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16),
+                   r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return max(max(r0, r1), max(r2, r3));
 }
 
 // The per-row scale of the reference: max(amax / 448, 1e-12) with IEEE
