@@ -287,7 +287,7 @@ __device__ __forceinline__ float wave_sum_f32(float v)
 }
 
 // The block's pre-norm fused with the per-token quantization:
-//   rstd   = 1 / sqrt(sum_k x^2 / K + eps)                       (binary32)
+//   rstd   = rsqrt(sum_k x^2 / K + eps)     (binary32, v_rsq_f32: within 1 ulp, as rms_norm's rsqrt)
 //   n[k]   = bf16(fma(x[k] * rstd, f[k], shift[i][k]))   f = w (1 + scale[i]),
 //                                                         (x[k] * rstd) * w[k] without a table
 //   y, s   = the quantize_rows arithmetic on n
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
 #pragma unroll
             for (int w = 1; w < WPR; ++w) ss += ssum[w];
         }
-        const float rstd = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+        const float rstd = __builtin_amdgcn_rsqf(ss / (float)p.K + p.eps);   // v_rsq_f32 (1 ulp)
         float mf = 0.0f;                             // row maximum of |n| (binary32)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
