@@ -18,9 +18,12 @@ Prints ONE JSON line:
               every config's kernel-equivalents at full size
   extra       the quantizer's HBM rate, the weight requantizer (plain and with the fused
               rank-64 LoRA merge), the other DiT GEMMs, the ms of one block's four
-              linears, the H3-width shapes and the pointwise kernels
+              linears, the H3-width shapes and the pointwise kernels; each HBM-bound
+              kernel also against a bare read + write stream of its own bytes
+              (`stream_GB/s`, `of_stream`), the rate this part gives for that traffic
 """
 import argparse
+import functools
 import itertools
 import json
 import os
@@ -148,6 +151,48 @@ def _time_region(fn, reps):
         ev[2 * i + 1].record()
     torch.cuda.synchronize()
     return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
+
+
+def _stream_probe():
+    """The bare-stream probe library (built beside libvdnfp8.so), or None if absent."""
+    import ctypes
+    path = os.path.join(ROOT, "vdn-minimax-h3_amd", "vdn_fp8", "libvdnprobe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    P = ctypes.c_void_p
+    lib.vdn_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, ctypes.c_int64, P,
+                                     ctypes.c_int, P]
+    lib.vdn_stream_probe.restype = ctypes.c_int
+    return lib
+
+
+def _stream_rate(lib, src, dst, read_bytes, write_bytes, nt_store, rotate=1, reps=10):
+    """GB/s of a bare stream moving a kernel's bytes: read_bytes read and write_bytes
+    written (1 KiB pieces, the read : write ratio rounded to 1, 2 or 4), stores
+    non-temporal or cached as the kernel's are, the source rotated over `rotate` disjoint
+    copies when the kernel's input is (so that it comes from HBM). Best of four grid
+    sizes, each timed as the kernels are (_time_region)."""
+    import ctypes
+    import torch
+    kr = max(1, round(read_bytes / write_bytes))
+    units = int(write_bytes // 1024)
+    rb, wb = units * kr * 1024, units * 1024
+    if rotate * rb > src.numel() or wb > dst.numel():
+        raise ValueError("stream probe buffers too small")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    best = 0.0
+    for grid in (1024, 2048, 4096, 8192):
+        srcs = itertools.cycle([src.data_ptr() + i * rb for i in range(rotate)])
+
+        def call():
+            rc = lib.vdn_stream_probe(kr, 1, int(nt_store), ctypes.c_void_p(next(srcs)), units,
+                                      ctypes.c_void_p(dst.data_ptr()), grid, stream)
+            if rc:
+                raise RuntimeError(f"vdn_stream_probe failed ({rc})")
+        ms = _time_region(call, reps)
+        best = max(best, (rb + wb) / (ms * 1e-3) / 1e9)
+    return best
 
 
 def _make_linear(w, b, dev, lora=None):
@@ -560,6 +605,29 @@ def main():
         extra["qk_prep_q"] = {"shape": [M, 40, 128], "ms": round(ms, 4), "GB/s": round(gbs, 1),
                               "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         del qkv_out, qv
+        # each HBM-bound kernel against a bare stream of its own read and write bytes
+        probe = _stream_probe()
+        if probe is not None:
+            src = torch.empty(1900 << 20, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty(460 << 20, dtype=torch.uint8, device=dev)
+            rate = functools.partial(_stream_rate, probe, src, dst)
+            nt_q = M * 13824 >= (256 << 20)          # the quantizers' non-temporal code stores
+            nw_, kw_ = extra["requantize_weight"]["shape"]
+            pats = {
+                ("quantize_rows", "pre_norm_quantize"): rate(2 * M * K, M * K + 4 * M, False),
+                ("requantize_weight", "lora_merge_requantize"): rate(2 * nw_ * kw_, nw_ * kw_ + 4 * nw_, False,
+                                                                     rotate=3),
+                ("quantize_rows_13824",): rate(2 * M * 13824, M * 13824 + 4 * M, nt_q),
+                ("swiglu_quantize_h3",): rate(4 * M * 14336, M * 14336 + 4 * M, True),
+                ("post_gated_residual",): rate(2 * M * K * 2, M * K * 2, True),
+                ("qk_prep_q",): rate(M * 5120 * 2, M * 5120 * 2, True),
+            }
+            for names, gbs in pats.items():
+                for n_ in names:
+                    if n_ in extra and "GB/s" in extra[n_]:
+                        extra[n_]["stream_GB/s"] = round(gbs, 1)
+                        extra[n_]["of_stream"] = round(extra[n_]["GB/s"] / gbs, 4)
+            del src, dst
         extra["gpu_clock"] = _gpu_clock()
     line["extra"] = extra
     if not args.no_cpu_baseline:

@@ -25,6 +25,10 @@ CSRC = os.path.join(_ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
 LIB_NAME = "libvdnfp8.so"
 LIB_PATH = os.path.join(_PKG, LIB_NAME)
+# The bare-stream probe bench.py sets the row kernels' rates against (not part of
+# the C ABI; built alongside, loaded by bench.py only).
+PROBE_SOURCE = "stream_probe.hip"
+PROBE_PATH = os.path.join(_PKG, "libvdnprobe.so")
 
 SOURCES = ["capi.hip", "quantize.hip", "lora_requant.hip", "gemm.hip", "qk_prep.hip", "block_ops.hip"]
 HEADERS = ["vdn_common.h"]             # in csrc/
@@ -116,6 +120,22 @@ def build(verbose=False, csrc=CSRC, include=INCLUDE, out=LIB_PATH):
             raise RuntimeError(f"linking {LIB_NAME} failed:\n{r.stderr}")
         # Copy next to the target, then rename: a process that already mapped
         # the old library keeps a consistent file.
+        shutil.copyfile(tmp_lib, out + ".tmp")
+        os.replace(out + ".tmp", out)
+    if out == LIB_PATH:
+        build_probe()
+    return out
+
+
+def build_probe(csrc=CSRC, out=PROBE_PATH):
+    """Compile the bare-stream probe into libvdnprobe.so. Returns its path."""
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="vdnprobe_build_") as tmp:
+        tmp_lib = os.path.join(tmp, os.path.basename(out))
+        r = subprocess.run([cc, *HIPCC_FLAGS, "-shared", os.path.join(csrc, PROBE_SOURCE), "-o", tmp_lib],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {PROBE_SOURCE}:\n{r.stderr}")
         shutil.copyfile(tmp_lib, out + ".tmp")
         os.replace(out + ".tmp", out)
     return out
