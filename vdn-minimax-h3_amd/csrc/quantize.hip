@@ -305,8 +305,9 @@ __device__ __forceinline__ float wave_sum_f32(float v)
 // flight while the current one is computed. The per-column factors f and the
 // shift (binary32) stay in VGPRs and are formed again only when the table row
 // changes (a frame of tokens shares one), so a row costs its own bytes and
-// three binary32 operations per element before the rounding. The waves-per-EU
-// bound holds the kernel to 168 VGPRs, so three waves share each SIMD.
+// three binary32 operations per element before the rounding. Up to five chunks
+// per lane, the waves-per-EU bound holds the kernel to 168 VGPRs, so three waves
+// share each SIMD (wider rows need more registers and run two).
 template <int CPL, int WPR, bool NT, bool AFFINE, bool QUANT>
 __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CPL <= 5 ? 3 : 1))) void k_norm_quant_blocks(NormArgs p, int64_t rb)
 {
