@@ -70,6 +70,20 @@ def test_pre_quantize_weight_and_table(device, M, K, T):
     _check(x, device, w, sc, sh, idx)
 
 
+@pytest.mark.parametrize("M,K,T,frames", [(4096, 5120, 21, True), (700, 4096, 3, True), (999, 3072, 7, True),
+                                          (1000, 3072, 5, False), (5, 5120, 2, False)])
+def test_pre_quantize_frames(device, M, K, T, frames):
+    """Table rows by frame (contiguous runs of tokens, the factors of a block's first and
+    last rows then serve every row) and at random (rows whose table row neither serves)."""
+    rng = np.random.default_rng(M + K + T)
+    x = _rand(rng, (M, K), 1.0)
+    w = _rand(rng, K, 0.1, 1.0)
+    sc = _rand(rng, (T, K), 0.3)
+    sh = _rand(rng, (T, K), 0.3)
+    idx = np.arange(M) * T // M if frames else rng.integers(0, T, M)
+    _check(x, device, w, sc, sh, idx)
+
+
 def test_pre_quantize_dit_rows(device):
     """The QKV activation's shape with its outlier channels, eps of the H3 norms."""
     from vdn_fp8 import workloads

@@ -14,6 +14,8 @@
 // contiguous.
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "vdn_common.h"
 
 namespace vdn {
@@ -472,6 +474,215 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
     }
 }
 
+// The per-column factors of the pre-norm for one 16-byte chunk q of table row ti:
+// f = w (1 + scale[ti]) and the shift (w alone and zero without a table); chunks
+// past K read as zeros.
+template <bool AFFINE>
+__device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int q, int rowbytes, float (&f)[8],
+                                             float (&h)[8])
+{
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.weight ? p.weight : p.x), 0, p.weight ? rowbytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t scs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(AFFINE ? p.mod_scale + ti * p.ldmod : p.x), 0, AFFINE ? rowbytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t shs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(AFFINE ? p.mod_shift + ti * p.ldmod : p.x), 0, AFFINE ? rowbytes : 0, 0x00020000);
+    const uint32_t off = (uint32_t)q * 16u;
+    const uint4 wv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+    const uint4 sc = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(scs, off, 0, 0));
+    const uint4 sh = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(shs, off, 0, 0));
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, sw[4] = {sc.x, sc.y, sc.z, sc.w}, hw[4] = {sh.x, sh.y, sh.z, sh.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float w0 = p.weight ? bf16_lo(ww[e]) : 1.0f, w1 = p.weight ? bf16_hi(ww[e]) : 1.0f;
+        f[2 * e] = AFFINE ? w0 * (1.0f + bf16_lo(sw[e])) : w0;
+        f[2 * e + 1] = AFFINE ? w1 * (1.0f + bf16_hi(sw[e])) : w1;
+        h[2 * e] = AFFINE ? bf16_lo(hw[e]) : 0.0f;
+        h[2 * e + 1] = AFFINE ? bf16_hi(hw[e]) : 0.0f;
+    }
+}
+
+// The same pre-norm + quantization, one wave per row, for rows of up to 64 CPL
+// chunks: a workgroup of W waves per CU walks a contiguous block of
+// rows, wave w taking rows w, w + W, .. of it (W waves), the next one's loads in
+// flight while a row is computed. The per-column factors sit in LDS for two table
+// rows -- those of the block's first and last rows, so every row of a block that
+// spans at most two frames of tokens finds its own; any other row forms its
+// factors from the tables itself -- so the registers hold only the rows, and a
+// row needs no exchange with another wave: its sum of squares and maximum are
+// wave reductions. Chunk q of a row is lane q % 64's chunk q / 64; the factor
+// slots keep the low and high four values of each chunk apart, so the 64 lanes'
+// 16-byte reads cover consecutive addresses.
+// Waves per workgroup: three per SIMD while the two row buffers leave room (168
+// VGPRs), two for rows of more than 512 chunks.
+constexpr int norm_row_waves(int cpl) { return cpl <= 8 ? 12 : 8; }
+// Rows in flight per wave besides the one computed (two, in the registers two waves
+// per SIMD leave at 64 chunks x 10, measured 0.0911 ms against 0.0891 ms with one).
+constexpr int norm_row_lookahead(int) { return 1; }
+template <int CPL, bool NT, bool AFFINE, bool QUANT>
+__global__ __launch_bounds__(norm_row_waves(CPL) * kLanes) void k_norm_quant_rows(NormArgs p, int64_t rb)
+{
+    constexpr int kNormRowWaves = norm_row_waves(CPL), LA = norm_row_lookahead(CPL);
+    constexpr int NQ = CPL * kLanes;
+    __shared__ float4 sf[2][2][NQ], sh[2][2][NQ];
+    const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int64_t row0 = (int64_t)blockIdx.x * rb;
+    const int64_t row_end = min(p.M, row0 + rb);
+    const int nch = (int)(p.K >> 3);
+    const int rowbytes = nch * 16;
+    // the lane's part of every row offset; the chunk's part (a multiple of 1 KiB) goes
+    // in the instructions' scalar offset
+    const uint32_t lane16 = (uint32_t)lane * 16u;
+    auto uniform = [](int64_t v) -> int64_t {
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+    auto load_row = [&](int64_t row, uint4 (&v)[CPL]) {
+        const bool valid = row < row_end;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.x + (valid ? row : 0) * p.ldx)), 0, valid ? rowbytes : 0, 0x00020000);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+            v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, lane16, c * kLanes * 16,
+                                                                                  kBufferLoadOnce));
+    };
+    auto table_row = [&](int64_t row) -> int64_t {
+        if (!AFFINE || !p.mod_index || row >= row_end) return 0;
+        const int32_t ti = __builtin_amdgcn_readfirstlane(p.mod_index[row]);
+        return min(max((int64_t)ti, (int64_t)0), p.mod_rows - 1);
+    };
+
+    uint4 vbuf[LA + 1][CPL];                         // buffer j: rows j, j + LA + 1, .. of this wave
+#pragma unroll
+    for (int j = 0; j < LA; ++j) load_row(row0 + wave + j * kNormRowWaves, vbuf[j]);   // in flight while the slots fill
+    const int64_t t0 = table_row(row0), t1 = table_row(row_end - 1);
+    for (int q = threadIdx.x; q < NQ; q += kNormRowWaves * kLanes) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+            float f[8], h[8];
+            norm_factors<AFFINE>(p, sl ? t1 : t0, q, rowbytes, f, h);
+            sf[sl][0][q] = make_float4(f[0], f[1], f[2], f[3]);
+            sf[sl][1][q] = make_float4(f[4], f[5], f[6], f[7]);
+            sh[sl][0][q] = make_float4(h[0], h[1], h[2], h[3]);
+            sh[sl][1][q] = make_float4(h[4], h[5], h[6], h[7]);
+        }
+    }
+    __syncthreads();
+
+    auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL]) {
+        const int64_t row = uniform(row_in);
+        load_row(row + LA * kNormRowWaves, vn);      // into the buffer the previous row freed
+        __builtin_amdgcn_sched_barrier(0);
+        const bool valid = row < row_end;
+        const int64_t ti = table_row(row);
+        const int slot = !valid || ti == t0 ? 0 : ti == t1 ? 1 : -1;   // wave-uniform
+        float ssp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ssp[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4[e]),
+                                                         __builtin_bit_cast(bf16x2_t, w4[e]), ssp[e], false);
+        }
+        const float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
+        const float rstd = __builtin_amdgcn_rsqf(ss / (float)p.K + p.eps);   // v_rsq_f32 (1 ulp)
+        float mf = 0.0f;                             // row maximum of |n| (binary32)
+        auto norm_chunk = [&](int c, const float (&f)[8], const float (&h)[8]) {
+            const uint32_t xw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float a = bf16_lo(xw[e]) * rstd, b = bf16_hi(xw[e]) * rstd;
+                if (AFFINE) {
+                    a = __builtin_fmaf(a, f[2 * e], h[2 * e]);
+                    b = __builtin_fmaf(b, f[2 * e + 1], h[2 * e + 1]);
+                } else {
+                    a *= f[2 * e];
+                    b *= f[2 * e + 1];
+                }
+                o[e] = pack_bf16x2(a, b);
+                mf = __builtin_elementwise_maximum(
+                    mf, __builtin_elementwise_maximum(__builtin_fabsf(a), __builtin_fabsf(b)));
+            }
+            // chunks past K hold zeros (x = 0, f = 0, shift = 0): nothing to the maximum
+            v[c] = make_uint4(o[0], o[1], o[2], o[3]);
+        };
+        if (slot >= 0) {
+            // the factors from the slot, each chunk's read one chunk ahead of its use (the
+            // scheduling barriers keep the compiler from hoisting every read, and the
+            // registers they would hold, to the top)
+            float f[2][8], h[2][8];
+            auto read = [&](int c, float (&fo)[8], float (&ho)[8]) {
+                const int q = lane + kLanes * c;
+                const float4 f0 = sf[slot][0][q], f1 = sf[slot][1][q];
+                fo[0] = f0.x; fo[1] = f0.y; fo[2] = f0.z; fo[3] = f0.w; fo[4] = f1.x; fo[5] = f1.y; fo[6] = f1.z; fo[7] = f1.w;
+                if (AFFINE) {
+                    const float4 h0 = sh[slot][0][q], h1 = sh[slot][1][q];
+                    ho[0] = h0.x; ho[1] = h0.y; ho[2] = h0.z; ho[3] = h0.w; ho[4] = h1.x; ho[5] = h1.y; ho[6] = h1.z; ho[7] = h1.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ho[e] = 0.0f;
+                }
+            };
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                read(c, f[0], h[0]);
+                norm_chunk(c, f[0], h[0]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            // a table row outside both slots: the factors from the tables, chunk by chunk
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                float f[8], h[8];
+                norm_factors<AFFINE>(p, ti, lane + kLanes * c, rowbytes, f, h);
+                norm_chunk(c, f, h);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.normed ? p.normed + (valid ? row : 0) * p.ldn : nullptr)), 0,
+            (valid && p.normed) ? rowbytes : 0, 0x00020000);
+        if (!QUANT) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16, c * kLanes * 16,
+                                                       NT ? kBufferLoadOnce : 0);
+            return;
+        }
+        const uint32_t mbits = wave_max_u32(pack_bf16x2(mf, 0.0f) & 0x7fffu);
+        const float scale = row_scale(bf16_to_f32((uint16_t)mbits));
+        if (valid && lane == 0) p.y_scale[row] = scale;
+        const float r = 1.0f / scale;
+        const bool finite = __builtin_isfinite(scale);
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform((int64_t)(p.y + (valid ? row : 0) * p.ldy)), 0, valid ? nch * 8 : 0, 0x00020000);
+        auto out_chunk = [&](int c, uint2 q) {
+            if (p.normed)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16, c * kLanes * 16,
+                                                       NT ? kBufferLoadOnce : 0);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2_t, q), yrs, lane16 / 2, c * kLanes * 8, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        if (finite) {                                // one uniform branch per row
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) out_chunk(c, quantize_chunk<false, false>(v[c], scale, r));
+        } else {                                     // a row holding inf or NaN: IEEE division
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) out_chunk(c, quantize_chunk<false, true>(v[c], scale, r));
+        }
+    };
+    // groups of LA + 1 rows, buffer j always holding the group's row j
+    for (int64_t r = row0 + wave; r < row_end; r += (LA + 1) * kNormRowWaves) {
+#pragma unroll
+        for (int j = 0; j <= LA; ++j)
+            if (j == 0 || r + j * kNormRowWaves < row_end)
+                one_row(r + j * kNormRowWaves, vbuf[j], vbuf[(j + LA) % (LA + 1)]);
+    }
+}
+
 // Wide rows (K > 8192 in the H3 FFN: 14336): WPR waves share a row, each holding
 // every WPR-th 1 KiB slice of it, so the binary32 activations fit in registers at
 // a useful occupancy; the row maximum is combined through LDS.
@@ -669,6 +880,31 @@ namespace {
 // workgroup, kNormWavesPerCU waves per CU; false when no instantiated chunk count
 // covers the row.
 constexpr int kNormWavesPerCU = 12;
+// k_norm_quant_rows: one workgroup per CU (fewer for short inputs), each walking a
+// contiguous block of rows.
+template <bool QUANT>
+void launch_norm_rows(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStream_t st)
+{
+    const bool nt = p.normed && M * nch * 16 >= kNtStoreBytes;   // the normed bf16 output
+    const bool affine = p.mod_scale != nullptr;
+    auto go = [&](auto cpl) {
+        constexpr int n = decltype(cpl)::value, waves = norm_row_waves(n);
+        const int64_t wgs = min((int64_t)cus, (M + waves - 1) / waves);
+        const int64_t rb = (M + wgs - 1) / wgs;
+        const dim3 grid((unsigned)((M + rb - 1) / rb)), block(waves * kLanes);
+        if (affine) {
+            if (nt) hipLaunchKernelGGL((k_norm_quant_rows<n, true, true, QUANT>), grid, block, 0, st, p, rb);
+            else hipLaunchKernelGGL((k_norm_quant_rows<n, false, true, QUANT>), grid, block, 0, st, p, rb);
+        } else {
+            if (nt) hipLaunchKernelGGL((k_norm_quant_rows<n, true, false, QUANT>), grid, block, 0, st, p, rb);
+            else hipLaunchKernelGGL((k_norm_quant_rows<n, false, false, QUANT>), grid, block, 0, st, p, rb);
+        }
+    };
+    if (nch <= 6 * kLanes) go(std::integral_constant<int, 6>{});
+    else if (nch <= 8 * kLanes) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 10>{});
+}
+
 template <int WPR, bool QUANT>
 bool launch_norm_blocks(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStream_t st)
 {
@@ -722,6 +958,12 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     // 8192, four beyond
     const int cus = device_cus();
     if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "norm_quantize_rows: cannot query the device's compute units");
+    // rows of 2049-5120 elements: one wave per row, the factors in LDS
+    if (nch > 4 * kLanes && nch <= 10 * kLanes) {
+        if (y) launch_norm_rows<true>(nch, M, p, cus, stream);
+        else launch_norm_rows<false>(nch, M, p, cus, stream);
+        return check_launch("norm_quantize_rows");
+    }
     bool ok;
     if (y) ok = nch <= 4 * kLanes    ? launch_norm_blocks<1, true>(nch, M, p, cus, stream)
                 : nch <= 16 * kLanes ? launch_norm_blocks<2, true>(nch, M, p, cus, stream)
