@@ -71,7 +71,8 @@ def test_pre_quantize_weight_and_table(device, M, K, T):
 
 
 @pytest.mark.parametrize("M,K,T,frames", [(4096, 5120, 21, True), (700, 4096, 3, True), (999, 3072, 7, True),
-                                          (1000, 3072, 5, False), (5, 5120, 2, False)])
+                                          (1000, 3072, 5, False), (5, 5120, 2, False), (2000, 5376, 4, True),
+                                          (600, 7168, 3, True), (300, 6144, 3, False)])
 def test_pre_quantize_frames(device, M, K, T, frames):
     """Table rows by frame (contiguous runs of tokens, the factors of a block's first and
     last rows then serve every row) and at random (rows whose table row neither serves)."""

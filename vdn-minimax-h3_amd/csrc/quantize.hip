@@ -503,7 +503,7 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 }
 
 // The same pre-norm + quantization, one wave per row, for rows of up to 64 CPL
-// chunks: a workgroup of W waves per CU walks a contiguous block of
+// chunks (CPL <= 14: the DiT's 5120 and H3's 5376 and 7168): a workgroup of W waves per CU walks a contiguous block of
 // rows, wave w taking rows w, w + W, .. of it (W waves), the next one's loads in
 // flight while a row is computed. The per-column factors sit in LDS for two table
 // rows -- those of the block's first and last rows, so every row of a block that
@@ -902,7 +902,9 @@ void launch_norm_rows(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStr
     };
     if (nch <= 6 * kLanes) go(std::integral_constant<int, 6>{});
     else if (nch <= 8 * kLanes) go(std::integral_constant<int, 8>{});
-    else go(std::integral_constant<int, 10>{});
+    else if (nch <= 10 * kLanes) go(std::integral_constant<int, 10>{});
+    else if (nch <= 12 * kLanes) go(std::integral_constant<int, 12>{});
+    else go(std::integral_constant<int, 14>{});
 }
 
 template <int WPR, bool QUANT>
@@ -958,8 +960,8 @@ extern "C" int vdn_fp8_norm_quantize_rows(const void* x, int64_t M, int64_t K, i
     // 8192, four beyond
     const int cus = device_cus();
     if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "norm_quantize_rows: cannot query the device's compute units");
-    // rows of 2049-5120 elements: one wave per row, the factors in LDS
-    if (nch > 4 * kLanes && nch <= 10 * kLanes) {
+    // rows of 2049-7168 elements: one wave per row, the factors in LDS
+    if (nch > 4 * kLanes && nch <= 14 * kLanes) {
         if (y) launch_norm_rows<true>(nch, M, p, cus, stream);
         else launch_norm_rows<false>(nch, M, p, cus, stream);
         return check_launch("norm_quantize_rows");
