@@ -95,8 +95,10 @@ def test_pre_quantize_dit_rows(device):
            rng.integers(0, 2, x.shape[0]), eps=1e-6)
 
 
-def test_pre_quantize_zero_and_constant_rows(device):
-    K = 512
+@pytest.mark.parametrize("K", [512, 5120, 7168])
+def test_pre_quantize_zero_and_constant_rows(device, K):
+    """Both kernels (one wave group per row up to 2048 elements, one wave per row with the
+    factors in LDS for 2049-7168)."""
     x = np.zeros((4, K), np.float32)
     x[1] = 3.0
     x[2] = -1e-20
