@@ -493,19 +493,32 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // buffer offset voff + soff (soff wave-uniform) land at LDS byte lds + 16 L.
 // Inline assembly, so that the compiler does not make every later LDS read wait
 // for it; the kernel waits on vmcnt itself. M0 carries the LDS address (restored
-// afterwards); s_nop covers the M0-write -> LDS-DMA hazard.
+// afterwards); s_nop covers the M0-write -> LDS-DMA hazard. kNT: non-temporal
+// (data read exactly once, such as the weight).
+template <bool kNT = false>
 __device__ __forceinline__ void copy16_to_lds(i32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff)
 {
     uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-        : "memory");
+    if constexpr (kNT)
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, %4 offen nt lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+            : "memory");
+    else
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+            : "memory");
 }
 
 __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
@@ -554,10 +567,11 @@ __device__ __forceinline__ void static_for(F&& f)
 // data registers. Without them the compiler placed a VALU write of the first
 // data register two instructions after such a store, and the store sent the new
 // value for the last four lanes of each 16-lane quarter (seen as wrong codes in
-// the first dword of those lanes).
+// the first dword of those lanes). kNT: non-temporal.
+template <bool kNT = false>
 __device__ __forceinline__ void store16_settled(i32x4_t v, __amdgpu_buffer_rsrc_t rs, uint32_t off, int soff)
 {
-    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, soff, kNT ? 2 : 0);
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7");
     __builtin_amdgcn_sched_barrier(0);
@@ -613,11 +627,14 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     const uint32_t ldw2 = (uint32_t)(p.ldw * 2), k2 = (uint32_t)(p.K * 2);
     const uint32_t w_lrow = (uint32_t)h * ldw2, w_lpc = (uint32_t)((nl ^ h) << 4);
     const uint32_t a_lrow = (uint32_t)h * k2, a_lpc = (uint32_t)((nl ^ (4 * h)) << 4);
+    // W is read once (non-temporal copies); the codes are stored non-temporally too
+    // (read by later GEMMs, not by the next kernel): [15360, 5120] rank 64 with W from
+    // HBM 52.9 us against 57.6 us with both cached
     auto copy_w1 = [&](i32x4_t wrs, int c, int st, int i) {
         const int d = kWCopies * wave + i;
         uint32_t so = (uint32_t)(2 * d) * ldw2;
         asm volatile("" : "+s"(so));   // the chunk's part added here, not kept per chunk
-        copy16_to_lds(wrs, lds_base + (uint32_t)(st * kWStage + d * 1024),
+        copy16_to_lds<true>(wrs, lds_base + (uint32_t)(st * kWStage + d * 1024),
                       (w_lpc ^ (uint32_t)(((2 * d) & 15) << 4)) + w_lrow, so + (uint32_t)(c * kRowB));
     };
     auto copy_a1 = [&](int c, int st, int i) {
@@ -872,7 +889,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         auto store_piece = [&](int c0, int j) {
             const int row = kRowsPerStore * (kPartC * wave + j) + srow;
             const uint32_t off = ((int64_t)c0 * kChunk + sbyte < p.K) ? (uint32_t)(row * p.ldq + sbyte) : kDropped;
-            store16_settled(__builtin_bit_cast(i32x4_t, pend[j]), qr, off, c0 * kChunk);
+            store16_settled<true>(__builtin_bit_cast(i32x4_t, pend[j]), qr, off, c0 * kChunk);
         };
         // Part q's codes go to buffer q % 2 while part q - 1's pieces are stored; then
         // (all of part q in LDS, every wave past its reads of part q - 1) part q's pieces
