@@ -78,6 +78,17 @@ struct GemmArgs {
     int group_m;   // m-tiles per group of the tile order
 };
 
+// bf16(v) as binary32 in one conversion: v into the high half, zero into the low
+// half (written as assembly: the compiler turns the zero-low form back into a
+// low-half conversion and a permute). Its operand is a VALU result, never an MFMA
+// accumulator read directly.
+__device__ __forceinline__ float round_bf16_hi(float v)
+{
+    uint32_t d;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(d) : "v"(v));
+    return __builtin_bit_cast(float, d);
+}
+
 // gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3):
 // exp(-2u) = 2^t with t = v (A + B v^2), A = -2 sqrt(2/pi) log2(e), B = 0.044715 A
 // (the constants folded so that t costs three operations and exp one).
@@ -460,23 +471,42 @@ void k_gemm_fp8(GemmArgs p)
                 for (int q = 0; q < 4; ++q) {
                     const int t = 2 * th + t2;
                     const float* sw = hsw[t2][q];
-                    uint32_t r01 = pack_bf16x2(acc[t][u][4 * q] * (sxm * sw[0]), acc[t][u][4 * q + 1] * (sxm * sw[1]));
-                    uint32_t r23 = pack_bf16x2(acc[t][u][4 * q + 2] * (sxm * sw[2]), acc[t][u][4 * q + 3] * (sxm * sw[3]));
-                    asm volatile("" : "+v"(r01), "+v"(r23));
-                    if (decltype(with_bias)::value) {
-                        const float* bb = hb[t2][q];
-                        r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
-                        r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
+                    // A rounding to bf16 that the bias add or GELU reads is one conversion per
+                    // value (round_bf16_hi: no unpacking); the last one converts the stored
+                    // pairs. The gate kernels keep the packed pairs and unpack them (one value
+                    // per conversion there made the compiler spill).
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[t][u][4 * q + e] * (sxm * sw[e]);
+                    uint32_t r01, r23;
+                    if (EPI != VDN_FP8_EPI_GATE) {
+                        if (decltype(with_bias)::value) {
+                            const float* bb = hb[t2][q];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = round_bf16_hi(v[e]) + bb[e];
+                        }
+                        if (EPI == VDN_FP8_EPI_GELU_TANH) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(round_bf16_hi(v[e]));   // of the bf16 output
+                        }
+                        r01 = pack_bf16x2(v[0], v[1]);
+                        r23 = pack_bf16x2(v[2], v[3]);
                         asm volatile("" : "+v"(r01), "+v"(r23));
-                    }
-                    if (EPI == VDN_FP8_EPI_GELU_TANH) {
-                        r01 = pack_bf16x2(gelu_tanh(bf16_lo(r01)), gelu_tanh(bf16_hi(r01)));
-                        r23 = pack_bf16x2(gelu_tanh(bf16_lo(r23)), gelu_tanh(bf16_hi(r23)));
-                    }
-                    if (EPI == VDN_FP8_EPI_GATE && FAST) {   // broadcast gate row, no residual
-                        const float* gg = hg[t2][q];
-                        r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
-                        r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
+                    } else {
+                        r01 = pack_bf16x2(v[0], v[1]);
+                        r23 = pack_bf16x2(v[2], v[3]);
+                        asm volatile("" : "+v"(r01), "+v"(r23));
+                        if (decltype(with_bias)::value) {
+                            const float* bb = hb[t2][q];
+                            r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
+                            r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
+                            asm volatile("" : "+v"(r01), "+v"(r23));
+                        }
+                        if (FAST) {   // broadcast gate row, no residual
+                            const float* gg = hg[t2][q];
+                            r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
+                            r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
+                        }
                     }
                     *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
                 }
