@@ -78,17 +78,6 @@ struct GemmArgs {
     int group_m;   // m-tiles per group of the tile order
 };
 
-// bf16(v) as binary32 in one conversion: v into the high half, zero into the low
-// half (written as assembly: the compiler turns the zero-low form back into a
-// low-half conversion and a permute). Its operand is a VALU result, never an MFMA
-// accumulator read directly.
-__device__ __forceinline__ float round_bf16_hi(float v)
-{
-    uint32_t d;
-    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(d) : "v"(v));
-    return __builtin_bit_cast(float, d);
-}
-
 // gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3):
 // exp(-2u) = 2^t with t = v (A + B v^2), A = -2 sqrt(2/pi) log2(e), B = 0.044715 A
 // (the constants folded so that t costs three operations and exp one).

@@ -781,9 +781,10 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
                     copy_j(cn, d);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                uint32_t dl = pack_bf16x2(a[2 * d] * p.lora_scale, a[2 * d + 1] * p.lora_scale);
-                asm volatile("" : "+v"(dl));
-                const float lo = bf16_lo(wr[c][d]) + bf16_lo(dl), hi = bf16_hi(wr[c][d]) + bf16_hi(dl);
+                // bf16(delta) as binary32, one conversion per value (its operand the
+                // scale multiply, not the accumulator itself)
+                const float dlo = round_bf16_hi(a[2 * d] * p.lora_scale), dhi = round_bf16_hi(a[2 * d + 1] * p.lora_scale);
+                const float lo = bf16_lo(wr[c][d]) + dlo, hi = bf16_hi(wr[c][d]) + dhi;
                 uint32_t m = pack_bf16x2(lo, hi);
                 asm volatile("" : "+v"(m));
                 wr[c][d] = m;

@@ -49,6 +49,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 
 __device__ __forceinline__ float round_bf16(float v) { return bf16_lo(pack_bf16x2(v, 0.0f)); }
 
+// The same rounding in one conversion: v into the high half, zero into the low half,
+// so the word is bf16(v) as binary32 with no unpacking (written as assembly: the
+// compiler turns the zero-low form back into a low-half conversion and a permute).
+// Its operand must be a VALU result, never an MFMA accumulator read directly (inline
+// assembly escapes the compiler's MFMA-to-VALU wait states).
+__device__ __forceinline__ float round_bf16_hi(float v)
+{
+    uint32_t d;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(d) : "v"(v));
+    return __builtin_bit_cast(float, d);
+}
+
 // 16-byte load of data read exactly once (activations streamed through a
 // kernel): non-temporal, so the stream does not displace cached lines that are
 // read again (the activation quantizer on [32760, 5120]: 0.080 ms against
