@@ -515,14 +515,19 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 // 16-byte reads cover consecutive addresses.
 // Waves per workgroup: three per SIMD while the two row buffers leave room (168
 // VGPRs), two for rows of more than 512 chunks.
-constexpr int norm_row_waves(int cpl) { return cpl <= 8 ? 12 : 8; }
+// With the table (the affine form) at 640 chunks, twelve fit once the next row's loads
+// go out after the row's normalization instead of before (0.0877 against 0.0898 ms with
+// eight waves and the early loads).
+constexpr int norm_row_waves(int cpl, bool affine) { return cpl <= 8 || (cpl == 10 && affine) ? 12 : 8; }
+constexpr bool norm_row_late_load(int cpl, bool affine) { return cpl > 8 && norm_row_waves(cpl, affine) == 12; }
 // Rows in flight per wave besides the one computed (two, in the registers two waves
 // per SIMD leave at 64 chunks x 10, measured 0.0911 ms against 0.0891 ms with one).
 constexpr int norm_row_lookahead(int) { return 1; }
 template <int CPL, bool NT, bool AFFINE, bool QUANT>
-__global__ __launch_bounds__(norm_row_waves(CPL) * kLanes) void k_norm_quant_rows(NormArgs p, int64_t rb)
+__global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_quant_rows(NormArgs p, int64_t rb)
 {
-    constexpr int kNormRowWaves = norm_row_waves(CPL), LA = norm_row_lookahead(CPL);
+    constexpr int kNormRowWaves = norm_row_waves(CPL, AFFINE), LA = norm_row_lookahead(CPL);
+    constexpr bool kLate = norm_row_late_load(CPL, AFFINE);
     constexpr int NQ = CPL * kLanes;
     __shared__ float4 sf[2][2][NQ], sh[2][2][NQ];
     const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
@@ -572,8 +577,10 @@ __global__ __launch_bounds__(norm_row_waves(CPL) * kLanes) void k_norm_quant_row
 
     auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL]) {
         const int64_t row = uniform(row_in);
-        load_row(row + LA * kNormRowWaves, vn);      // into the buffer the previous row freed
-        __builtin_amdgcn_sched_barrier(0);
+        if (!kLate) {
+            load_row(row + LA * kNormRowWaves, vn);  // into the buffer the previous row freed
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const bool valid = row < row_end;
         const int64_t ti = table_row(row);
         const int slot = !valid || ti == t0 ? 0 : ti == t1 ? 1 : -1;   // wave-uniform
@@ -641,6 +648,11 @@ __global__ __launch_bounds__(norm_row_waves(CPL) * kLanes) void k_norm_quant_row
                 norm_chunk(c, f, h);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        }
+        if (kLate) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(row + LA * kNormRowWaves, vn);  // once the row's factors no longer hold registers
+            __builtin_amdgcn_sched_barrier(0);
         }
         const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)uniform((int64_t)(p.normed ? p.normed + (valid ? row : 0) * p.ldn : nullptr)), 0,
@@ -889,17 +901,18 @@ void launch_norm_rows(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStr
     const bool nt = p.normed && M * nch * 16 >= kNtStoreBytes;   // the normed bf16 output
     const bool affine = p.mod_scale != nullptr;
     auto go = [&](auto cpl) {
-        constexpr int n = decltype(cpl)::value, waves = norm_row_waves(n);
-        const int64_t wgs = min((int64_t)cus, (M + waves - 1) / waves);
-        const int64_t rb = (M + wgs - 1) / wgs;
-        const dim3 grid((unsigned)((M + rb - 1) / rb)), block(waves * kLanes);
-        if (affine) {
-            if (nt) hipLaunchKernelGGL((k_norm_quant_rows<n, true, true, QUANT>), grid, block, 0, st, p, rb);
-            else hipLaunchKernelGGL((k_norm_quant_rows<n, false, true, QUANT>), grid, block, 0, st, p, rb);
-        } else {
-            if (nt) hipLaunchKernelGGL((k_norm_quant_rows<n, true, false, QUANT>), grid, block, 0, st, p, rb);
-            else hipLaunchKernelGGL((k_norm_quant_rows<n, false, false, QUANT>), grid, block, 0, st, p, rb);
-        }
+        constexpr int n = decltype(cpl)::value;
+        auto launch = [&](auto af) {
+            constexpr bool AF = decltype(af)::value;
+            constexpr int waves = norm_row_waves(n, AF);
+            const int64_t wgs = min((int64_t)cus, (M + waves - 1) / waves);
+            const int64_t rb = (M + wgs - 1) / wgs;
+            const dim3 grid((unsigned)((M + rb - 1) / rb)), block(waves * kLanes);
+            if (nt) hipLaunchKernelGGL((k_norm_quant_rows<n, true, AF, QUANT>), grid, block, 0, st, p, rb);
+            else hipLaunchKernelGGL((k_norm_quant_rows<n, false, AF, QUANT>), grid, block, 0, st, p, rb);
+        };
+        if (affine) launch(std::true_type{});
+        else launch(std::false_type{});
     };
     if (nch <= 6 * kLanes) go(std::integral_constant<int, 6>{});
     else if (nch <= 8 * kLanes) go(std::integral_constant<int, 8>{});
