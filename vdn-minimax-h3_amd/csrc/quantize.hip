@@ -503,9 +503,9 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 }
 
 // The same pre-norm + quantization, one wave per row, for rows of up to 64 CPL
-// chunks (CPL <= 14: the DiT's 5120 and H3's 5376 and 7168): a workgroup of W waves per CU walks a contiguous block of
-// rows, wave w taking rows w, w + W, .. of it (W waves), the next one's loads in
-// flight while a row is computed. The per-column factors sit in LDS for two table
+// chunks (CPL <= 14: the DiT's 5120 and H3's 5376 and 7168). One workgroup of W
+// waves per CU walks a contiguous block of rows, wave w taking rows w, w + W, ..
+// of it, the next one's loads in flight while a row is computed. The per-column factors sit in LDS for two table
 // rows -- those of the block's first and last rows, so every row of a block that
 // spans at most two frames of tokens finds its own; any other row forms its
 // factors from the tables itself -- so the registers hold only the rows, and a
@@ -514,10 +514,10 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 // slots keep the low and high four values of each chunk apart, so the 64 lanes'
 // 16-byte reads cover consecutive addresses.
 // Waves per workgroup: three per SIMD while the two row buffers leave room (168
-// VGPRs), two for rows of more than 512 chunks.
-// With the table (the affine form) at 640 chunks, twelve fit once the next row's loads
-// go out after the row's normalization instead of before (0.0877 against 0.0898 ms with
-// eight waves and the early loads).
+// VGPRs), two for rows of more than 512 chunks -- except with the table (the affine
+// form) at 640 chunks, where twelve fit once the next row's loads go out after the
+// row's normalization instead of before (0.0880 against 0.0907 ms with eight waves
+// and the early loads).
 constexpr int norm_row_waves(int cpl, bool affine) { return cpl <= 8 || (cpl == 10 && affine) ? 12 : 8; }
 constexpr bool norm_row_late_load(int cpl, bool affine) { return cpl > 8 && norm_row_waves(cpl, affine) == 12; }
 // Rows in flight per wave besides the one computed (two, in the registers two waves
