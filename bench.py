@@ -583,6 +583,18 @@ def main():
         ms = _time_region(lambda: vdn_fp8.pre_quantize(x, nw, 1e-6, nsc, nsh, nidx), reps)
         gbs = wl.quant_bytes(M, K) / (ms * 1e-3) / 1e9
         extra["pre_norm_quantize"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
+        # the same at the H3 width (one rank's 13107 tokens of hidden 5376, 5 frames)
+        Mh3, Kh3, fh3 = 13107, 5376, 5
+        xh3 = torch.randn(Mh3, Kh3, generator=g).to(torch.bfloat16).to(dev)
+        nw3 = (1 + 0.05 * torch.randn(Kh3, generator=g)).to(torch.bfloat16).to(dev)
+        nsc3 = (0.2 * torch.randn(fh3, Kh3, generator=g)).to(torch.bfloat16).to(dev)
+        nsh3 = (0.2 * torch.randn(fh3, Kh3, generator=g)).to(torch.bfloat16).to(dev)
+        nidx3 = (torch.arange(Mh3) * fh3 // Mh3).to(torch.int32).to(dev)
+        ms = _time_region(lambda: vdn_fp8.pre_quantize(xh3, nw3, 1e-6, nsc3, nsh3, nidx3), reps)
+        gbs = wl.quant_bytes(Mh3, Kh3) / (ms * 1e-3) / 1e9
+        extra["pre_norm_quantize_h3"] = {"shape": [Mh3, Kh3], "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                         "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
+        del xh3
         # the block's gated residual add (`post`) over [M, 5120] with a 2-row gate table
         br_ = torch.randn(M, K, device=dev).to(torch.bfloat16)
         gtab = (2 * torch.rand(2, K, device=dev)).to(torch.bfloat16)
@@ -615,6 +627,7 @@ def main():
             nw_, kw_ = extra["requantize_weight"]["shape"]
             pats = {
                 ("quantize_rows", "pre_norm_quantize"): rate(2 * M * K, M * K + 4 * M, False),
+                ("pre_norm_quantize_h3",): rate(2 * 13107 * 5376, 13107 * 5376 + 4 * 13107, False),
                 ("requantize_weight", "lora_merge_requantize"): rate(2 * nw_ * kw_, nw_ * kw_ + 4 * nw_, False,
                                                                      rotate=3),
                 ("quantize_rows_13824",): rate(2 * M * 13824, M * 13824 + 4 * M, nt_q),
