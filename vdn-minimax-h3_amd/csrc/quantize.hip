@@ -565,6 +565,7 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
     for (int q = threadIdx.x; q < NQ; q += kNormRowWaves * kLanes) {
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
+            if (sl == 1 && t1 == t0) break;          // one table row: slot 1 is never chosen
             float f[8], h[8];
             norm_factors<AFFINE>(p, sl ? t1 : t0, q, rowbytes, f, h);
             sf[sl][0][q] = make_float4(f[0], f[1], f[2], f[3]);
