@@ -153,18 +153,73 @@ def _time_region(fn, reps):
     return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
 
 
-def _stream_probe():
-    """The bare-stream probe library (built beside libvdnfp8.so), or None if absent."""
+def _probe_lib():
+    """The measurement probes (bare stream, bare MFMA loop; built beside libvdnfp8.so), or
+    None if absent."""
     import ctypes
     path = os.path.join(ROOT, "vdn-minimax-h3_amd", "vdn_fp8", "libvdnprobe.so")
     if not os.path.exists(path):
         return None
     lib = ctypes.CDLL(path)
-    P = ctypes.c_void_p
-    lib.vdn_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, ctypes.c_int64, P,
-                                     ctypes.c_int, P]
-    lib.vdn_stream_probe.restype = ctypes.c_int
+    P, I = ctypes.c_void_p, ctypes.c_int
+    lib.vdn_stream_probe.argtypes = [I, I, I, P, ctypes.c_int64, P, I, P]
+    lib.vdn_stream_probe.restype = I
+    lib.vdn_mfma_probe.argtypes = [I, P, P, ctypes.c_int64, ctypes.c_int64, I, I, P, P]
+    lib.vdn_mfma_probe.restype = I
     return lib
+
+
+def _mfma_ceiling(lib, xq, wq, blocks, grid, reps):
+    """The bare fp8 MFMA loop (the GEMM's grid, K-loop instruction mix and LDS fragment
+    reads, no copies, no epilogue) on the GEMM's own codes, on uniform codes, and with the
+    fragments held in registers: ms, TFLOP/s, fraction of the dense peak, and the clock and
+    power amd-smi reads while it runs back to back."""
+    import ctypes
+    import torch
+    out = torch.empty(grid * 256, dtype=torch.float32, device=xq.device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    flop = grid * 4 * blocks * 32 * (2 * 32 * 32 * 64)
+    tiles = min(xq.shape[0], wq.shape[0]) // 256
+    res = {}
+    for name, mode in (("random_codes", 0), ("uniform_codes", 1), ("random_codes_registers_only", 2)):
+        def call():
+            rc = lib.vdn_mfma_probe(mode, ctypes.c_void_p(xq.data_ptr()), ctypes.c_void_p(wq.data_ptr()),
+                                    xq.stride(0), tiles, blocks, grid, ctypes.c_void_p(out.data_ptr()), stream)
+            if rc:
+                raise RuntimeError(f"vdn_mfma_probe failed ({rc})")
+        ms = _time_region(call, reps)
+        tf = flop / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP8_TFLOPS, 4),
+                     "under_load": _under_load(call, seconds=1.5)}
+    res["flop"] = flop
+    return res
+
+
+def _torch_rate(read_bytes, write_bytes, rotate=1, reps=10):
+    """GB/s of a torch library kernel moving a kernel's bytes with the same read : write
+    ratio: copy_ (1:1), torch.add(a, b, out=c) (2:1), torch.sum over groups of four (4:1),
+    on bf16 tensors, the sources rotated over `rotate` disjoint copies when the kernel's
+    input is (so that it comes from HBM)."""
+    import torch
+    kr = max(1, round(read_bytes / write_bytes))
+    n = int(write_bytes // 2) // 256 * 256          # bf16 elements written
+    dev = torch.device("cuda:0")
+    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    srcs = [torch.empty(kr * n, dtype=torch.bfloat16, device=dev).normal_() for _ in range(rotate)]
+    rot = itertools.cycle(srcs)
+    if kr == 1:
+        fn = lambda: dst.copy_(next(rot))
+    elif kr == 2:
+        def fn():
+            s_ = next(rot)
+            torch.add(s_[:n], s_[n:], out=dst)
+    elif kr == 4:
+        fn = lambda: torch.sum(next(rot).view(-1, 4, 256), dim=1, out=dst.view(-1, 256))
+    else:
+        raise ValueError(f"no torch kernel for a {kr}:1 mix")
+    ms = _time_region(fn, reps)
+    del srcs, dst
+    return (kr * n * 2 + n * 2) / (ms * 1e-3) / 1e9
 
 
 def _stream_rate(lib, src, dst, read_bytes, write_bytes, nt_store, rotate=1, reps=10):
@@ -274,7 +329,13 @@ def cpu_baseline(draws):
         wm, tm = timed(lambda: O.lora_merge(draws["w5"], draws["a5"], draws["b5"], draws["s5"]))
         _, tw = timed(lambda: O.quantize_weight(wm))
         per["cfg5_lora_merge_requantize"] = {"merge_ms": round(tm, 1), "quantize_w_ms": round(tw, 1)}
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
     return {"value": round(value, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "host_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "threads_note": "threads = min(16, os.cpu_count()): the GPU box's CPU share is 16 per GPU",
             "sample": "the whole QKV step (quantize X [32760, 5120], dequantized fp32 matmul against W "
                       "[15360, 5120] + bias) once at full size; cfg1 median of 3 after a warm-up; the other "
                       "configs' kernel-equivalents once each at full size (oracle C quantizers and merge, numpy "
@@ -511,6 +572,36 @@ def main():
                                            "under_load": _under_load(lambda: lin_u.forward_quantized(qu, sx0))}
         extra["gemm_qkv_under_load"] = _under_load(lambda: lin.forward_quantized(qx0, sx0))
         del lin_u, qu
+        # the bare MFMA loop on the same codes: the matrix cores' own rate on this data
+        probe = _probe_lib()
+        if probe is not None:
+            cus = torch.cuda.get_device_properties(dev).multi_processor_count
+            tiles_m, tiles_n = (M + 255) // 256, (N + 255) // 256
+            blocks = (tiles_m * tiles_n + cus - 1) // cus * (K // 128)     # the GEMM's K blocks per CU
+            ceil = _mfma_ceiling(probe, qx0.view(torch.uint8), lin.weight_fp8.view(torch.uint8), blocks, cus, reps)
+            rnd = ceil["random_codes"]["TFLOP/s"]
+            ceil["gemm_of_mfma_ceiling"] = round(gemm_tflops / rnd, 4)
+            extra["mfma_random_ceiling"] = ceil
+            line["roofline"]["of_mfma_ceiling"] = round(gemm_tflops / rnd, 4)
+        # the reference's own forward_quantized on the same codes: torch._scaled_mm with the
+        # rowwise scales (hipBLASLt here), then the bf16 bias add (fp8_linear.py:272-276)
+        try:
+            def ref_mm():
+                return torch._scaled_mm(qx0, lin.weight_fp8.t(), scale_a=sx0, scale_b=lin.weight_scale,
+                                        out_dtype=torch.bfloat16, use_fast_accum=True)
+            ref_mm()
+            torch.cuda.synchronize()
+            ms_mm = _time_region(ref_mm, reps)
+            ms_all = _time_region(lambda: ref_mm() + lin.bias, reps)
+            tf = flops / (ms_all * 1e-3) / 1e12
+            extra["torch_scaled_mm_qkv"] = {
+                "call": "torch._scaled_mm(x_fp8, weight_fp8.t(), scale_a=[M,1], scale_b=[1,N], "
+                        "out_dtype=bf16, use_fast_accum=True) + bias",
+                "ms": round(ms_all, 4), "scaled_mm_ms": round(ms_mm, 4), "TFLOP/s": round(tf, 1),
+                "frac": round(tf / PEAK_FP8_TFLOPS, 4), "ours_ms": round(gemm_ms, 4),
+                "ours_over_torch": round(ms_all / gemm_ms, 4)}
+        except RuntimeError as e:
+            extra["torch_scaled_mm_qkv"] = {"error": str(e).splitlines()[0][:300]}
         # the H3 model's widths at one rank's share of a sequence (13107 tokens): fused QKV
         # [21504 x 5376] + bias, FF projection [28672 x 5376] + bias, FF down [5376 x 14336]
         # with the block's gate table and residual
@@ -617,30 +708,38 @@ def main():
         extra["qk_prep_q"] = {"shape": [M, 40, 128], "ms": round(ms, 4), "GB/s": round(gbs, 1),
                               "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         del qkv_out, qv
-        # each HBM-bound kernel against a bare stream of its own read and write bytes
-        probe = _stream_probe()
+        # each HBM-bound kernel against a bare stream of its own read and write bytes, and
+        # against a torch library kernel with the same read : write mix
+        probe = _probe_lib()
+        nw_, kw_ = extra["requantize_weight"]["shape"]
+        mixes = {   # names: (read bytes, write bytes, non-temporal stores, source copies rotated)
+            ("quantize_rows", "pre_norm_quantize"): (2 * M * K, M * K + 4 * M, False, 1),
+            ("pre_norm_quantize_h3",): (2 * 13107 * 5376, 13107 * 5376 + 4 * 13107, False, 1),
+            ("requantize_weight", "lora_merge_requantize"): (2 * nw_ * kw_, nw_ * kw_ + 4 * nw_, False, 3),
+            ("quantize_rows_13824",): (2 * M * 13824, M * 13824 + 4 * M, M * 13824 >= (256 << 20), 1),
+            ("swiglu_quantize_h3",): (4 * M * 14336, M * 14336 + 4 * M, True, 1),
+            ("post_gated_residual",): (2 * M * K * 2, M * K * 2, True, 1),
+            ("qk_prep_q",): (M * 5120 * 2, M * 5120 * 2, True, 1),
+        }
         if probe is not None:
             src = torch.empty(1900 << 20, dtype=torch.uint8, device=dev).fill_(1)
             dst = torch.empty(460 << 20, dtype=torch.uint8, device=dev)
             rate = functools.partial(_stream_rate, probe, src, dst)
-            nt_q = M * 13824 >= (256 << 20)          # the quantizers' non-temporal code stores
-            nw_, kw_ = extra["requantize_weight"]["shape"]
-            pats = {
-                ("quantize_rows", "pre_norm_quantize"): rate(2 * M * K, M * K + 4 * M, False),
-                ("pre_norm_quantize_h3",): rate(2 * 13107 * 5376, 13107 * 5376 + 4 * 13107, False),
-                ("requantize_weight", "lora_merge_requantize"): rate(2 * nw_ * kw_, nw_ * kw_ + 4 * nw_, False,
-                                                                     rotate=3),
-                ("quantize_rows_13824",): rate(2 * M * 13824, M * 13824 + 4 * M, nt_q),
-                ("swiglu_quantize_h3",): rate(4 * M * 14336, M * 14336 + 4 * M, True),
-                ("post_gated_residual",): rate(2 * M * K * 2, M * K * 2, True),
-                ("qk_prep_q",): rate(M * 5120 * 2, M * 5120 * 2, True),
-            }
-            for names, gbs in pats.items():
+            for names, (rb_, wb_, nt_, rot_) in mixes.items():
+                gbs = rate(rb_, wb_, nt_, rotate=rot_)
                 for n_ in names:
                     if n_ in extra and "GB/s" in extra[n_]:
                         extra[n_]["stream_GB/s"] = round(gbs, 1)
                         extra[n_]["of_stream"] = round(extra[n_]["GB/s"] / gbs, 4)
             del src, dst
+        for names, (rb_, wb_, _, rot_) in mixes.items():
+            gbs = _torch_rate(rb_, wb_, rotate=rot_)
+            for n_ in names:
+                if n_ in extra and "GB/s" in extra[n_]:
+                    extra[n_]["torch_GB/s"] = round(gbs, 1)
+                    extra[n_]["of_torch"] = round(extra[n_]["GB/s"] / gbs, 4)
+        extra["torch_kernels"] = ("copy_ (1:1), torch.add(a, b, out=c) (2:1), torch.sum over groups of four (4:1), "
+                                  "bf16, the same bytes as each kernel")
         extra["gpu_clock"] = _gpu_clock()
     line["extra"] = extra
     if not args.no_cpu_baseline:

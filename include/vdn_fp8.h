@@ -19,8 +19,8 @@
  *   - Return 0 on success. A nonzero status leaves nothing launched, and
  *     vdn_fp8_last_error() returns the message (per host thread). Calls are
  *     re-entrant. The library's only mutable state is that message and a
- *     per-device cache of the compute-unit count, filled once under
- *     std::call_once.
+ *     per-device cache of the compute-unit count (an atomic per device; only
+ *     a successful query is kept, a failed one is retried by the next call).
  *   - Scales: x_scale / w_scale are binary32, one per row of X / W.
  *   - Table indices (gate_index, mod_index) outside the table are clamped into
  *     it; the reference's index_select raises on them instead (a deliberate

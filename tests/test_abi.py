@@ -144,3 +144,19 @@ def test_stale_library_is_refused(tmp_path):
     env = dict(os.environ, VDN_FP8_SOURCE_DIR=str(tmp_path))
     r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert "REFUSED" in r.stdout and "gemm.hip" in r.stdout, r.stdout + r.stderr
+
+
+def test_library_from_another_compiler_is_refused(tmp_path):
+    """The manifest records the compiler's identity: with another hipcc installed (a
+    stand-in script on HIPCC reporting another version) the same library does not load."""
+    import subprocess
+    import sys
+    fake = tmp_path / "hipcc"
+    fake.write_text("#!/bin/sh\necho 'HIP version: 0.0.0-other'\necho 'AMD clang version 0.0.0 (other)'\n")
+    fake.chmod(0o755)
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import vdn_fp8._lib as L\n"
+            "try:\n    L.load()\nexcept RuntimeError as e:\n    print('REFUSED', e)\n" % os.path.join(ROOT, "vdn-minimax-h3_amd"))
+    env = dict(os.environ, HIPCC=str(fake))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert "REFUSED" in r.stdout and "compiler" in r.stdout, r.stdout + r.stderr

@@ -70,6 +70,36 @@ def test_pre_within_one_ulp(device):
     assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s1, s2)
 
 
+@pytest.mark.parametrize("M,K", [(4000, 8192), (3200, 13824), (3200, 16384)])
+def test_pre_wide_rows_many_per_block(device, M, K):
+    """The norm-only pre-norm on rows that two or four waves share, with several rows per
+    workgroup (M above the resident wave groups): each row's partial sums of squares must
+    meet only its own row's, with one barrier per row in this form."""
+    print(f"pre wide M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M + K)
+    T = 3
+    # rows of very different magnitude, so a sum of squares taken from a neighbouring
+    # row would change the normed values by far more than a rounding
+    x = O.bf16_encode(rng.standard_normal((M, K), dtype=np.float32) *
+                      np.exp2(rng.integers(-6, 7, (M, 1))).astype(np.float32))
+    w = O.bf16_encode(1 + 0.1 * rng.standard_normal(K, dtype=np.float32))
+    sc = O.bf16_encode(0.2 * rng.standard_normal((T, K), dtype=np.float32))
+    sh = O.bf16_encode(0.2 * rng.standard_normal((T, K), dtype=np.float32))
+    idx = np.arange(M) * T // M
+    out = FB.pre(from_bits(x, device), from_bits(w, device), 1e-6, from_bits(sc, device), from_bits(sh, device),
+                 torch.from_numpy(idx).to(device))
+    torch.cuda.synchronize()
+    want, terms = O.norm_rows(x, w, 1e-6, sc, sh, idx, return_terms=True)
+    gv, wv = O.bf16_decode(bits(out)).astype(np.float64), O.bf16_decode(want).astype(np.float64)
+    assert np.all(np.abs(gv - wv) <= _ulp(np.maximum(np.abs(wv), terms)))
+    assert np.mean(bits(out) == want) >= 0.995
+    # the fused form (two barriers per row) gives the same normed bits
+    _, _, n2 = FB.pre_quantize(from_bits(x, device), from_bits(w, device), 1e-6, from_bits(sc, device),
+                               from_bits(sh, device), torch.from_numpy(idx).to(device), return_normed=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(n2), bits(out))
+
+
 # --------------------------------------------------------------------------------------
 # A small block with the reference block's structure (diffusers' MiniMaxH3 block as the
 # reference's fast_block_forward uses it): adaln_proj -> 6 chunks, norm1/norm2 RMSNorm,

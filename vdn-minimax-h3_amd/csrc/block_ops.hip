@@ -82,8 +82,8 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_gated_residual(
             if (RES) { lo = bf16_lo(rw[e]) + lo; hi = bf16_hi(rw[e]) + hi; }
             o[e] = pack_bf16x2(lo, hi);
         }
-        __builtin_amdgcn_raw_buffer_store_b128(i32x4_t{(int)o[0], (int)o[1], (int)o[2], (int)o[3]}, ors,
-                                               (c0 + j * kLanes) * 16u, 0, NT ? kStoreOnce : 0);
+        store_b128_settled<NT ? kStoreOnce : 0>(i32x4_t{(int)o[0], (int)o[1], (int)o[2], (int)o[3]}, ors,
+                                                (c0 + j * kLanes) * 16u, 0);
     }
 }
 

@@ -3,7 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <mutex>
+#include <atomic>
 
 #include "vdn_common.h"
 
@@ -27,28 +27,26 @@ int check_launch(const char* what)
     return VDN_FP8_OK;
 }
 
-// The CU count of each device, queried once per device (std::call_once: calls
-// from several host threads see one initialization and no torn value).
+// The CU count of each device, queried once per device: only a successful query
+// is kept (a failed one is retried by the next call), and concurrent first calls
+// from several host threads at worst both query and store the same value.
 namespace {
 constexpr int kMaxDevices = 64;
-std::once_flag g_cus_once[kMaxDevices];
-int g_cus[kMaxDevices];
+std::atomic<int> g_cus[kMaxDevices];
 }  // namespace
 
 int device_cus()
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev >= kMaxDevices) {
-        int n = 0;
-        return hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? n : 0;
+    if (dev < kMaxDevices) {
+        const int cached = g_cus[dev].load(std::memory_order_relaxed);
+        if (cached > 0) return cached;
     }
-    std::call_once(g_cus_once[dev], [dev]() {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-        g_cus[dev] = n;
-    });
-    return g_cus[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    if (dev < kMaxDevices) g_cus[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 int pick_cpl(int64_t nch)

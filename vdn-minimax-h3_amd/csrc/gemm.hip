@@ -31,8 +31,9 @@
 // epilogue stores 8 bytes (4 bf16) per lane.
 //
 // Tile order: workgroup b runs on XCD b % 8; tiles are renumbered so each XCD
-// walks a contiguous run of the tile space, grouped 8 m-tiles at a time, which
-// keeps the X and W slices its 32 CUs share resident in that XCD's L2.
+// walks a contiguous run of the tile space, grouped kGroupM (4) m-tiles at a time
+// (2 for narrow outputs over long rows), which keeps the X and W slices its 32 CUs
+// share resident in that XCD's L2.
 //
 // K % 128 != 0 goes to a second kernel (BK = 128, 16x16x128 MFMA, two stages)
 // whose last step is filled through VGPRs with zeros past K.
@@ -510,14 +511,18 @@ void k_gemm_fp8(GemmArgs p)
 #pragma unroll
             for (int i = 0; i < 4; ++i) pv[i] = *reinterpret_cast<const uint4*>(stg + (8 * i + rl) * kStgRow + (cc << 4));
         };
+        // (the four offsets first, then the four stores back to back and their wait states)
         auto store_slab = [&](int th, int u) {
             const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
             const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
+            uint32_t off[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t off = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off, 0, kStoreNT);
-            }
+            for (int i = 0; i < 4; ++i) off[i] = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off[i], 0, kStoreNT);
+            settle_stores();
         };
 #pragma unroll
         for (int sidx = 0; sidx < 8; ++sidx) {

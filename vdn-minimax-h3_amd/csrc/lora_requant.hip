@@ -64,6 +64,14 @@ constexpr uint32_t kDropped = 0x80000000u;
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ i32x2_t u32x2(uint32_t a, uint32_t b) { return i32x2_t{(int)a, (int)b}; }
+
+// Bytes of `rows` rows of W (bf16, row stride ld elements) up to the end of the last
+// row's K elements: the caller's W may end right after them, so no read range of a
+// descriptor reaches past (ld - K) padding of the last row.
+__device__ __forceinline__ int64_t w_span_bytes(int64_t rows, int64_t ld, int64_t K)
+{
+    return rows > 0 ? ((rows - 1) * ld + K) * 2 : 0;
+}
 __device__ __forceinline__ i32x4_t u32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 {
     return i32x4_t{(int)a, (int)b, (int)c, (int)d};
@@ -175,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
         const int64_t n0 = (int64_t)rtc * kTileRows;
         const int64_t rows = rt < p.row_tiles ? min(p.N - n0, (int64_t)kTileRows) : 0;
         const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.w + n0 * p.ldw), 0, (int)(rows * p.ldw * 2), 0x00020000);
+            (void*)(p.w + n0 * p.ldw), 0, (int)w_span_bytes(rows, p.ldw, p.K), 0x00020000);
 #pragma unroll
         for (int c = 0; c < kGroups; ++c) {
             const uint32_t off = (uint32_t)((nr * p.ldw + k0 + 64 * c + 16 * g) * 2);
@@ -326,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void k_lora_stripes(Args p)
                 const uint32_t off = in ? (uint32_t)((nr * p.ldw + k) * 2) : kDropped;
                 if (p.wm16) {
                     __builtin_amdgcn_raw_buffer_store_b128(u32x4(wm[0], wm[1], wm[2], wm[3]), mr, off, 0, 0);
-                    __builtin_amdgcn_raw_buffer_store_b128(u32x4(wm[4], wm[5], wm[6], wm[7]), mr, off + 16, 0, 0);
+                    store_b128_settled<0>(u32x4(wm[4], wm[5], wm[6], wm[7]), mr, off + 16, 0);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
@@ -563,20 +571,6 @@ __device__ __forceinline__ void static_for(F&& f)
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// A 16-byte buffer store, then wait states before anything can overwrite its
-// data registers. Without them the compiler placed a VALU write of the first
-// data register two instructions after such a store, and the store sent the new
-// value for the last four lanes of each 16-lane quarter (seen as wrong codes in
-// the first dword of those lanes). kNT: non-temporal.
-template <bool kNT = false>
-__device__ __forceinline__ void store16_settled(i32x4_t v, __amdgpu_buffer_rsrc_t rs, uint32_t off, int soff)
-{
-    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, soff, kNT ? 2 : 0);
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_nop 7");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 template <int RP, int NCH, bool BVEC, bool MERGED>
 __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
 {
@@ -655,7 +649,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
     // W descriptor of a group (empty past the last group: reads zeros, touches no memory)
     auto w_rsrc = [&](int64_t n0) {
         const int64_t rows = n0 < p.N ? min(p.N - n0, rpg) : 0;
-        return rsrc_words(p.w + n0 * p.ldw, rows * p.ldw * 2);
+        return rsrc_words(p.w + n0 * p.ldw, w_span_bytes(rows, p.ldw, p.K));
     };
     // Transposing reads: lane (group G = lane / 16, j = (lane / 4) % 4, q = lane % 4)
     // addresses rank row 8 h + j (+ 16 s + 4 half) at the four columns MFMA rows
@@ -869,8 +863,8 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
             if (MERGED) {
                 const uint32_t wv = (uint32_t)((nl * p.ldw + lcol) * 2);
                 const uint32_t off = voff_at(wv, c);
-                store16_settled(u32x4(wr[c][0], wr[c][1], wr[c][2], wr[c][3]), mr, off, c * kRowB);
-                store16_settled(u32x4(wr[c][4], wr[c][5], wr[c][6], wr[c][7]), mr, off + 16, c * kRowB);
+                store_b128_settled<0>(u32x4(wr[c][0], wr[c][1], wr[c][2], wr[c][3]), mr, off, c * kRowB);
+                store_b128_settled<0>(u32x4(wr[c][4], wr[c][5], wr[c][6], wr[c][7]), mr, off + 16, c * kRowB);
             }
             __builtin_amdgcn_sched_barrier(0);
         };
@@ -890,7 +884,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
         auto store_piece = [&](int c0, int j) {
             const int row = kRowsPerStore * (kPartC * wave + j) + srow;
             const uint32_t off = ((int64_t)c0 * kChunk + sbyte < p.K) ? (uint32_t)(row * p.ldq + sbyte) : kDropped;
-            store16_settled<true>(__builtin_bit_cast(i32x4_t, pend[j]), qr, off, c0 * kChunk);
+            store_b128_settled<kBufferLoadOnce>(__builtin_bit_cast(i32x4_t, pend[j]), qr, off, c0 * kChunk);
         };
         // Part q's codes go to buffer q % 2 while part q - 1's pieces are stored; then
         // (all of part q in LDS, every wave past its reads of part q - 1) part q's pieces

@@ -315,7 +315,10 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
 {
     // one group of WPR waves (one row at a time) per workgroup: the barriers that
     // combine a row's partial sums hold up only the waves of that row
-    __shared__ float ssum[WPR];
+    // The partial sums of squares alternate between two slots by row parity: the
+    // norm-only form meets one barrier per row, so a wave may write the next row's
+    // sum while another still reads this row's.
+    __shared__ float ssum[2][WPR];
     __shared__ uint32_t smax[WPR];
     const int lane = threadIdx.x & (kLanes - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int part = wave % WPR;
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
     load_row(row0, va);
     int64_t cur_ti = table_row(row0);
     load_factors(cur_ti);
-    auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL]) {
+    auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL], int par) {
         const int64_t row = uniform(row_in);
         load_row(row + 1, vn);                       // the next row, in flight meanwhile
         __builtin_amdgcn_sched_barrier(0);
@@ -404,11 +407,11 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
         }
         float ss = wave_sum_f32((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
         if (WPR > 1) {
-            if (lane == 0) ssum[wave] = ss;
+            if (lane == 0) ssum[par][wave] = ss;
             __syncthreads();
-            ss = ssum[0];
+            ss = ssum[par][0];
 #pragma unroll
-            for (int w = 1; w < WPR; ++w) ss += ssum[w];
+            for (int w = 1; w < WPR; ++w) ss += ssum[par][w];
         }
         const float rstd = __builtin_amdgcn_rsqf(ss / (float)p.K + p.eps);   // v_rsq_f32 (1 ulp)
         float mf = 0.0f;                             // row maximum of |n| (binary32)
@@ -440,8 +443,7 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
         if (!QUANT) {                                // the pre-norm alone (bf16 out)
 #pragma unroll
             for (int c = 0; c < CPL; ++c)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, chunk_off(c), 0,
-                                                       NT ? kBufferLoadOnce : 0);
+                store_b128_settled<NT ? kBufferLoadOnce : 0>(__builtin_bit_cast(i32x4_t, v[c]), nrs, chunk_off(c), 0);
             return;
         }
         // bf16 rounding is monotone and odd, so the bf16 of the binary32 maximum of |n|
@@ -463,14 +465,14 @@ __global__ __launch_bounds__(WPR * kLanes) __attribute__((amdgpu_waves_per_eu(CP
         for (int c = 0; c < CPL; ++c) {
             const uint32_t off = chunk_off(c);
             if (p.normed)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, off, 0, NT ? kBufferLoadOnce : 0);
+                store_b128_settled<NT ? kBufferLoadOnce : 0>(__builtin_bit_cast(i32x4_t, v[c]), nrs, off, 0);
             const uint2 q = finite ? quantize_chunk<false, false>(v[c], scale, r) : quantize_chunk<false, true>(v[c], scale, r);
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2_t, q), yrs, off / 2, 0, 0);
         }
     };
     for (int64_t i = 0; i < rb; i += 2) {
-        one_row(row0 + i, va, vb);
-        if (i + 1 < rb) one_row(row0 + i + 1, vb, va);
+        one_row(row0 + i, va, vb, 0);
+        if (i + 1 < rb) one_row(row0 + i + 1, vb, va, 1);
     }
 }
 
@@ -661,8 +663,8 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
         if (!QUANT) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16, c * kLanes * 16,
-                                                       NT ? kBufferLoadOnce : 0);
+                store_b128_settled<NT ? kBufferLoadOnce : 0>(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16,
+                                                             c * kLanes * 16);
             return;
         }
         const uint32_t mbits = wave_max_u32(pack_bf16x2(mf, 0.0f) & 0x7fffu);
@@ -674,8 +676,8 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
             (void*)uniform((int64_t)(p.y + (valid ? row : 0) * p.ldy)), 0, valid ? nch * 8 : 0, 0x00020000);
         auto out_chunk = [&](int c, uint2 q) {
             if (p.normed)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16, c * kLanes * 16,
-                                                       NT ? kBufferLoadOnce : 0);
+                store_b128_settled<NT ? kBufferLoadOnce : 0>(__builtin_bit_cast(i32x4_t, v[c]), nrs, lane16,
+                                                             c * kLanes * 16);
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2_t, q), yrs, lane16 / 2, c * kLanes * 8, 0);
             __builtin_amdgcn_sched_barrier(0);
         };

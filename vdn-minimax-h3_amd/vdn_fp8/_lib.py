@@ -3,13 +3,14 @@
 The library is required: there is no CPU or torch fallback for any entry point.
 Loading fails loudly when the shared library is missing, was built for another ABI
 version, or was built from sources other than the ones beside it (its embedded
-source manifest, vdn_fp8_build_info, must match the csrc/ and include/ files on disk).
+source manifest, vdn_fp8_build_info, must match the csrc/ and include/ files on disk,
+the build flags and, where hipcc is installed, the compiler's identity).
 """
 import ctypes
 import json
 import os
 
-from .build import CSRC, INCLUDE, LIB_PATH, source_manifest
+from .build import CSRC, INCLUDE, LIB_PATH, compiler_id, source_manifest
 
 ABI_VERSION = 2
 
@@ -50,16 +51,23 @@ def _check_sources(lib, path):
     src_root = os.environ.get("VDN_FP8_SOURCE_DIR")
     csrc, include = (os.path.join(src_root, "csrc"), os.path.join(src_root, "include")) if src_root \
         else (CSRC, INCLUDE)
+    # the compiler is compared where one is installed (a machine without hipcc cannot
+    # rebuild, and checks the sources and flags alone)
+    compiler = compiler_id() or info.get("compiler", "unknown")
     try:
-        want = source_manifest(csrc, include)
+        want = source_manifest(csrc, include, compiler)
     except FileNotFoundError as e:
         raise RuntimeError(f"cannot check {path} against its sources ({e}); the fp8 library ships with "
                            "its csrc/ and include/ trees") from None
     if info.get("digest") != want["digest"]:
         stale = sorted(f for f, h in want["sources"].items() if info.get("sources", {}).get(f) != h)
+        if not stale and info.get("flags") != want["flags"]:
+            stale = ["build flags"]
+        if not stale and info.get("compiler") != want["compiler"]:
+            stale = [f"compiler ({info.get('compiler')!r}, installed {want['compiler']!r})"]
         raise RuntimeError(
             f"{path} was built from other sources than {csrc} / {include} "
-            f"(differs in: {', '.join(stale) or 'build flags'}): rebuild it (python "
+            f"(differs in: {', '.join(stale) or 'manifest'}): rebuild it (python "
             f"vdn-minimax-h3_amd/vdn_fp8/build.py, or __graft_entry__.build())")
     return info
 

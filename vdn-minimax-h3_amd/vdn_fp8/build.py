@@ -5,10 +5,11 @@
 Objects are compiled in a temporary directory (in parallel) and only the shared
 library lands next to this file, where the ctypes loader looks for it.
 
-The library carries the sha256 of every source it was built from (and of the flags),
-returned by vdn_fp8_build_info(); the loader compares it with the sources on disk and
-refuses a library built from other sources, so a stale build cannot stand in for the
-current kernels.
+The library carries the sha256 of every source it was built from (and of the flags, and
+the compiler's identity), returned by vdn_fp8_build_info(); the loader compares it with
+the sources on disk (and the installed hipcc, where there is one) and refuses a library
+built from other sources or by another compiler, so a stale build cannot stand in for
+the current kernels.
 """
 import concurrent.futures
 import hashlib
@@ -25,9 +26,10 @@ CSRC = os.path.join(_ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
 LIB_NAME = "libvdnfp8.so"
 LIB_PATH = os.path.join(_PKG, LIB_NAME)
-# The bare-stream probe bench.py sets the row kernels' rates against (not part of
+# The measurement probes bench.py sets the kernels' rates against -- a bare read +
+# write stream for the row kernels, a bare fp8 MFMA loop for the GEMM -- (not part of
 # the C ABI; built alongside, loaded by bench.py only).
-PROBE_SOURCE = "stream_probe.hip"
+PROBE_SOURCES = ["stream_probe.hip", "mfma_probe.hip"]
 PROBE_PATH = os.path.join(_PKG, "libvdnprobe.so")
 
 SOURCES = ["capi.hip", "quantize.hip", "lora_requant.hip", "gemm.hip", "qk_prep.hip", "block_ops.hip"]
@@ -54,15 +56,36 @@ def _sha256(path):
         return hashlib.sha256(f.read()).hexdigest()
 
 
-def source_manifest(csrc=CSRC, include=INCLUDE):
-    """{"sources": {file: sha256}, "flags": sha256, "digest": sha256 of all of it}: what
-    a library built from these files carries. Raises FileNotFoundError if a file is
-    missing."""
+_compiler_id = None
+
+
+def compiler_id():
+    """The compiler's identity, the "HIP version" and "clang version" lines of
+    `hipcc --version` (the kernels' exact wait counts and schedules depend on its
+    output), or None when no hipcc is installed."""
+    global _compiler_id
+    if _compiler_id is None:
+        try:
+            r = subprocess.run([hipcc(), "--version"], capture_output=True, text=True, timeout=60)
+        except (RuntimeError, OSError, subprocess.SubprocessError):
+            return None
+        lines = [ln.strip() for ln in r.stdout.splitlines() if "HIP version" in ln or "clang version" in ln]
+        _compiler_id = " | ".join(lines) if r.returncode == 0 and lines else "unknown"
+    return _compiler_id
+
+
+def source_manifest(csrc=CSRC, include=INCLUDE, compiler=None):
+    """{"sources": {file: sha256}, "flags": sha256, "compiler": str, "digest": sha256 of
+    all of it}: what a library built from these files, with these flags and this
+    compiler (compiler_id() unless given), carries. Raises FileNotFoundError if a file
+    is missing."""
     files = {name: _sha256(os.path.join(csrc, name)) for name in SOURCES + HEADERS}
     files.update({name: _sha256(os.path.join(include, name)) for name in PUBLIC_HEADERS})
     flags = hashlib.sha256(json.dumps([HIPCC_FLAGS, EXTRA_FLAGS], sort_keys=True).encode()).hexdigest()
-    body = json.dumps({"sources": files, "flags": flags}, sort_keys=True)
-    return {"sources": files, "flags": flags, "digest": hashlib.sha256(body.encode()).hexdigest()}
+    compiler = compiler if compiler is not None else (compiler_id() or "unknown")
+    body = json.dumps({"sources": files, "flags": flags, "compiler": compiler}, sort_keys=True)
+    return {"sources": files, "flags": flags, "compiler": compiler,
+            "digest": hashlib.sha256(body.encode()).hexdigest()}
 
 
 # The files that make each kernel family (its source plus the shared headers).
@@ -128,14 +151,14 @@ def build(verbose=False, csrc=CSRC, include=INCLUDE, out=LIB_PATH):
 
 
 def build_probe(csrc=CSRC, out=PROBE_PATH):
-    """Compile the bare-stream probe into libvdnprobe.so. Returns its path."""
+    """Compile the measurement probes into libvdnprobe.so. Returns its path."""
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="vdnprobe_build_") as tmp:
         tmp_lib = os.path.join(tmp, os.path.basename(out))
-        r = subprocess.run([cc, *HIPCC_FLAGS, "-shared", os.path.join(csrc, PROBE_SOURCE), "-o", tmp_lib],
-                           capture_output=True, text=True)
+        r = subprocess.run([cc, *HIPCC_FLAGS, "-shared", *(os.path.join(csrc, f) for f in PROBE_SOURCES),
+                            "-o", tmp_lib], capture_output=True, text=True)
         if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {PROBE_SOURCE}:\n{r.stderr}")
+            raise RuntimeError(f"hipcc failed on {', '.join(PROBE_SOURCES)}:\n{r.stderr}")
         shutil.copyfile(tmp_lib, out + ".tmp")
         os.replace(out + ".tmp", out)
     return out
