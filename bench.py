@@ -409,6 +409,12 @@ def _only(name, steps, warmup):
         th = torch.rand(wl.TOKENS, 64, device=dev) * 6.28
         cs, sn = torch.cat([th.cos(), th.cos()], 1), torch.cat([th.sin(), th.sin()], 1)
         fn = lambda: vdn_fp8.qk_prep(qv, nq, 1e-6, cs, sn)
+    elif name in ("gemm_h3_ff_down", "gemm_qkv"):
+        M_, N_, K_ = (13107, 5376, 14336) if name == "gemm_h3_ff_down" else (wl.TOKENS, wl.QKV, wl.HIDDEN)
+        gh = torch.Generator().manual_seed(13)
+        qx, sx = vdn_fp8.quantize_rows(torch.randn(M_, K_, generator=gh).to(torch.bfloat16).to(dev))
+        lin = _make_linear((0.02 * torch.randn(N_, K_, generator=gh)).to(torch.bfloat16), None, dev)
+        fn = lambda: lin.forward_quantized(qx, sx)
     else:
         raise SystemExit(f"unknown --only workload {name!r}")
     for _ in range(warmup):
@@ -427,7 +433,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time one workload's kernel alone (lora_requant, requant, "
-                    "quantize_5120, quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep)")
+                    "quantize_5120, quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep, gemm_h3_ff_down, "
+                    "gemm_qkv)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the fp8 linear path has no cross-GPU step "

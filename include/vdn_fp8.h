@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VDN_FP8_ABI_VERSION 2
+#define VDN_FP8_ABI_VERSION 3
 
 /* status codes */
 #define VDN_FP8_OK 0
@@ -152,6 +152,36 @@ int vdn_fp8_gemm(const void *xq, const float *x_scale, const void *wq, const flo
                  const void *bias, int epilogue, const void *gate, const int32_t *gate_index,
                  int64_t gate_rows, int64_t ldgate, const void *residual, int64_t ldres,
                  void *out, int64_t ldo, hipStream_t stream);
+
+/*
+ * Bytes of workspace vdn_fp8_gemm_ws takes for an [M, N, K] GEMM on the current
+ * device (0: the shape does not split). Only rows of K >= 8192 split: when the
+ * 256 x 256 output tiles leave a last round of at most half the compute units,
+ * those tiles run as several K slices whose binary32 partial sums go to the
+ * workspace (256 KiB per slice), then a reduction kernel sums them, slice by
+ * slice, and applies the epilogue.
+ * Replaces: nothing in the reference (torch._scaled_mm sizes its own workspace,
+ *           src/models/ops/fp8_linear.py:272); the query for the next call.
+ */
+int vdn_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int64_t *bytes);
+
+/*
+ * vdn_fp8_gemm with a caller-provided split-K workspace (device memory, 16-byte
+ * aligned, at least vdn_fp8_gemm_workspace_size bytes; NULL: no split, the same
+ * call as vdn_fp8_gemm). The summation order of an output depends only on K,
+ * its tile's position and the split, so a shape gives the same bits call after
+ * call; a split shape's last-round tiles sum their K slices in binary32 after
+ * the matrix cores, so their bits can differ from vdn_fp8_gemm's by a rounding.
+ * Replaces: Fp8Linear.forward_quantized, src/models/ops/fp8_linear.py:270-277,
+ *           as vdn_fp8_gemm does.
+ * Requires: as vdn_fp8_gemm; workspace_bytes >= the size query's answer.
+ */
+int vdn_fp8_gemm_ws(const void *xq, const float *x_scale, const void *wq, const float *w_scale,
+                    int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                    const void *bias, int epilogue, const void *gate, const int32_t *gate_index,
+                    int64_t gate_rows, int64_t ldgate, const void *residual, int64_t ldres,
+                    void *out, int64_t ldo, void *workspace, int64_t workspace_bytes,
+                    hipStream_t stream);
 
 /*
  * QK preparation between the q (or k) projection and attention: per-head

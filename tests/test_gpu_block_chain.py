@@ -12,7 +12,10 @@ Checked against the oracle chain on one row of every 256-row tile:
   (+ GELU) outputs within the GEMM tolerance of the oracle's dequantized matmul;
 - the FFN-up output, quantized again on the GPU, bit-exact with the oracle's codes of the
   same rows, and the FFN-down (+ gate) output within tolerance of the oracle's matmul of
-  those codes."""
+  those codes;
+- every output of the four linears identical to the reference's own call on this part
+  (torch._scaled_mm on the same codes, then its bias add and epilogue) or one rounding
+  chain apart."""
 import numpy as np
 import pytest
 import torch
@@ -21,7 +24,7 @@ import torch.nn as nn
 import oracle as O
 import vdn_fp8
 from conftest import bits, codes, from_bits
-from test_gpu_gemm import MAX_ABS, REL_L2, _tile_rows, bf16_ulp
+from test_gpu_gemm import MAX_ABS, REL_L2, _tile_rows, _vs_reference_call, bf16_ulp, reference_call
 from vdn_fp8 import workloads
 
 pytestmark = pytest.mark.gpu
@@ -107,3 +110,14 @@ def test_lora_block_chain(device):
     mid = [O.dequant_linear(hq, hs, wq, ws), O.dequant_linear(hq, hs, wq, ws)]
     _within("ffn-down + gate", O.bf16_decode(bits(y_dn[rows])), want, mid, None,
             max(1.0, float(np.abs(O.bf16_decode(g_bits)).max())))
+    # every output of the four linears against the reference's own call on this part
+    # (torch._scaled_mm on the same codes, then its bias add and epilogue)
+    for name, lin, y, q_, s_, epi in (("qkv", qkv, y_qkv, qx, sx, "none"),
+                                      ("attn-out + gate", out_l, y_out, qx, sx, "gate"),
+                                      ("ffn-up + gelu", up_l, h, qx, sx, "gelu_tanh"),
+                                      ("ffn-down + gate", dn_l, y_dn, qh, sh, "gate")):
+        rc = reference_call(q_, s_, lin, epi, gate if epi == "gate" else None)
+        if rc is not None:
+            print(name, end=": ", flush=True)
+            _vs_reference_call(y, rc)
+            del rc

@@ -6,7 +6,14 @@ max-abs <= 2e-2 of the reference's result: (qx * sx) @ (qw * sw)^T in float64, r
 to bf16 where the reference's op sequence rounds (the bf16 output of _scaled_mm, the
 bf16 bias add, the epilogue on the bf16 tensor). Against the UNROUNDED float64 result
 the bound is 3e-3: a correctly rounded bf16 output alone sits at rel-L2 ~1.7e-3 from it
-(bf16 keeps 8 significant bits), the reference's own double rounding at ~2.3e-3."""
+(bf16 keeps 8 significant bits), the reference's own double rounding at ~2.3e-3.
+
+Every output is also compared with the reference's own call on this part -- torch._scaled_mm
+with the rowwise scales and fast accumulation (hipBLASLt), the bias add and the epilogue in
+torch -- on the same codes: identical, or one rounding chain apart. The identical-output
+floors against the oracle follow from that call's own identical fraction on the same rows:
+the fp8 matrix cores accumulate with less precision than binary32, in hipBLASLt as here, so
+both flip ~1% of the bf16 roundings a float64 sum would give."""
 import numpy as np
 import pytest
 import torch
@@ -22,12 +29,81 @@ REL_L2 = 1e-3          # vs the reference's bf16 result
 MAX_ABS = 2e-2         # ... per element, or one bf16 ulp of the value where that is larger
 REL_L2_UNROUNDED = 3e-3   # vs the float64 result before any bf16 rounding (4e-3 with GELU:
                           # the reference rounds three times on that path)
+REF_CALL_SAME = 0.995     # identical outputs with the reference's own call on this part
+                          # (torch._scaled_mm on the same codes): measured >= 0.99999 where the
+                          # library walks K in 64-byte steps as this kernel does, 0.998 at
+                          # K = 13824 (the library's kernel for that shape groups the products
+                          # differently, and each MFMA aligns its 64 products to their largest)
 
 
 def bf16_ulp(v):
     """Spacing of bf16 values at |v| (2^-133 at zero and below the normal range)."""
     e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
     return 2.0 ** (e - 7)
+
+
+def reference_call(qx, sx, f, epilogue="none", gate=None, gate_index=None, residual=None, exact_gelu=True):
+    """The reference's own forward_quantized on this part, on the same codes:
+    torch._scaled_mm(x_fp8, weight_fp8.t(), scale_a=[M, 1], scale_b=[1, N], out_dtype=bf16,
+    use_fast_accum=True) -- hipBLASLt here -- then the bf16 bias add (fp8_linear.py:272-276),
+    then the epilogue on the bf16 tensor as the reference's callers apply it: F.gelu(tanh), or
+    the compiled gated residual bf16(residual + gate[idx] * v) (fused_block.py:47-49).
+    Returns (output, its rounding chain per element: one bf16 step at the GEMM output and
+    one at the bias add, times the epilogue's slope), or None if torch refuses the call (its
+    message printed)."""
+    try:
+        v = torch._scaled_mm(qx, f.weight_fp8.t(), scale_a=sx, scale_b=f.weight_scale,
+                             out_dtype=torch.bfloat16, use_fast_accum=True)
+    except RuntimeError as e:
+        print(f"torch._scaled_mm refused [{qx.shape[0]} x {f.out_features} x {qx.shape[1]}]: "
+              f"{str(e).splitlines()[0][:160]}", flush=True)
+        return None
+    chain = _ulp_t(v)
+    if f.bias is not None:
+        v = v + f.bias.detach()
+        chain += _ulp_t(v)
+    if epilogue == "gelu_tanh":
+        # F.gelu(tanh) on the bf16 tensor: evaluated accurately (float64, then one rounding)
+        # by default, or as torch itself evaluates it on a bf16 tensor on this part
+        # (exact_gelu=False), which flips ~3% of those roundings
+        v = torch.nn.functional.gelu(v.double() if exact_gelu else v, approximate="tanh").to(torch.bfloat16)
+        chain = 1.13 * chain + _ulp_t(v)
+    elif epilogue == "gate":
+        g = gate if gate.dim() == 2 else gate.reshape(1, -1)
+        idx = torch.zeros(v.shape[0], dtype=torch.long, device=v.device) if gate_index is None \
+            else gate_index.long().clamp(0, g.shape[0] - 1)
+        gv = g.float()[idx]
+        o = gv * v.float()
+        if residual is not None:
+            o = o + residual.float()
+        v = o.to(torch.bfloat16)
+        chain = gv.abs().clamp_min(1.0) * chain + _ulp_t(v)
+    return v, chain
+
+
+def _ulp_t(v):
+    """bf16 spacing at |v| (binary32 tensor)."""
+    return torch.exp2(torch.floor(torch.log2(v.float().abs().clamp_min(2.0 ** -126))) - 7)
+
+
+def _vs_reference_call(out, ref):
+    """Every output against the reference's own call: identical, or apart by at most
+    max(2e-2, the rounding chain each side may flip: twice the chain). (Where an output
+    cancels, the matrix cores' alignment error is relative to the largest product, not to
+    the output, so its chain bound is the absolute 2e-2.) Returns the identical fraction."""
+    r, chain = ref
+    diff = out.view(torch.int16) != r.view(torch.int16)
+    n_diff = int(diff.sum())
+    worst = 0.0
+    if n_diff:
+        bound = (2 * chain[diff]).clamp_min(MAX_ABS)
+        worst = float(((out.float()[diff] - r.float()[diff]).abs() / bound).max())
+    same = 1.0 - n_diff / out.numel()
+    print(f"vs the reference's own call (torch._scaled_mm, fast accumulation): identical={same:.6f} "
+          f"({n_diff} of {out.numel()} differ) worst/bound={worst:.2f}", flush=True)
+    assert worst <= 1.0, worst
+    assert same >= REF_CALL_SAME, same
+    return same
 
 
 def _linear(w_bits, b_bits, device):
@@ -52,6 +128,8 @@ def _check(x_bits, w_bits, b_bits, device, rows=None, **epi):
     if kw.get("gate_index") is not None:
         kw["gate_index"] = torch.from_numpy(kw["gate_index"]).to(device)
     out = f.forward_quantized(qx, sx, **kw)
+    ref = reference_call(qx, sx, f, epi.get("epilogue") or "none", kw.get("gate"), kw.get("gate_index"),
+                         kw.get("residual"))
     torch.cuda.synchronize()
     sel = slice(None) if rows is None else rows
     got = O.bf16_decode(bits(out))[sel]
@@ -94,7 +172,30 @@ def _check(x_bits, w_bits, b_bits, device, rows=None, **epi):
           + (f" |v| of those in [{vmag.min():.3g}, {vmag.max():.3g}]" if above.any() else ""), flush=True)
     assert rel <= REL_L2, rel
     assert worst <= 1.0, (mx, worst)
-    assert same >= 0.98, same
+    # The identical fraction against the float64 oracle: at least what the reference's own
+    # call on this part reaches on the same rows (the fp8 matrix cores' accumulation flips
+    # ~1% of the roundings against float64, as much in hipBLASLt as here), less four
+    # binomial standard deviations. Where torch refuses the shape, 0.98 (the lowest the
+    # reference's call reaches on the DiT and H3 configs, less a margin).
+    if ref is not None:
+        ref_rows = O.bf16_decode(bits(ref[0]))[sel]
+        same_ref = float(np.mean(ref_rows == want))
+        if epi.get("epilogue") == "gelu_tanh":
+            # the floor: the smaller of the two GELU evaluations of the reference's call
+            # (accurate, or torch's own on the bf16 tensor); this kernel's binary32 GELU
+            # (exp2 and reciprocal, argument error amplified for negative v) sits between
+            tg = reference_call(qx, sx, f, "gelu_tanh", exact_gelu=False)
+            same_tg = float(np.mean(O.bf16_decode(bits(tg[0]))[sel] == want))
+            print(f"identical with the oracle: the reference's call with torch's bf16 GELU {same_tg:.5f}",
+                  flush=True)
+            same_ref = min(same_ref, same_tg)
+        floor = same_ref - 4.0 * np.sqrt(max(same_ref * (1.0 - same_ref), 1e-12) / got.size)
+        print(f"identical with the oracle: ours {same:.5f}, the reference's call {same_ref:.5f} "
+              f"(floor {floor:.5f})", flush=True)
+        _vs_reference_call(out, ref)
+    else:
+        floor = 0.98
+    assert same >= floor, (same, floor)
     assert rel_exact <= (4e-3 if epi.get("epilogue") == "gelu_tanh" else REL_L2_UNROUNDED), rel_exact
     return got, want
 
@@ -105,7 +206,8 @@ def _screen_full(x_bits, w_bits, b_bits, device, epilogue="none", gate=None):
     by torch's fp32 matmul (a library GEMM; another summation order), then the same
     rounding points as the reference (bf16 output, bf16 bias add, epilogue on the bf16
     value). Each output must be within max(2e-2, the rounding chain) of it, rel-L2 <=
-    1e-3 over the whole output and >= 98% identical."""
+    1e-3 over the whole output, and identical as often as the reference's own call on this
+    part (torch._scaled_mm on the same codes) is to the same screen."""
     f = _linear(w_bits, b_bits, device)
     qx, sx = vdn_fp8.quantize_rows(from_bits(x_bits, device))
     kw = {}
@@ -150,7 +252,16 @@ def _screen_full(x_bits, w_bits, b_bits, device, epilogue="none", gate=None):
           f"max_abs={float(err.max()):.3e} identical={same:.5f} worst/bound={worst:.2f} above_2e-2={n_above}"
           + (f" |v| of those in [{float(vmag.min()):.3g}, {float(vmag.max()):.3g}]" if n_above else ""),
           flush=True)
-    assert rel <= REL_L2 and worst <= 1.0 and same >= 0.98, (rel, worst, same)
+    # identical fraction: at least the reference's own call's against the same screen (less
+    # four binomial standard deviations); 0.98 where torch refuses the shape
+    rc = reference_call(qx, sx, f, epilogue, kw.get("gate"))
+    floor = 0.98
+    if rc is not None:
+        same_ref = float((rc[0].float() == ref).float().mean())
+        floor = same_ref - 4.0 * (max(same_ref * (1.0 - same_ref), 1e-12) / ref.numel()) ** 0.5
+        print(f"identical with the binary32 screen: ours {same:.5f}, the reference's call {same_ref:.5f} "
+              f"(floor {floor:.5f})", flush=True)
+    assert rel <= REL_L2 and worst <= 1.0 and same >= floor, (rel, worst, same, floor)
 
 
 def _rand(rng, shape, std):
@@ -268,14 +379,20 @@ def test_gemm_gate_rows_paths(device):
     qx, sx = vdn_fp8.quantize_rows(from_bits(x, device))
     resbuf = from_bits(_rand(rng, (M, N + 4), 1.0), device)
     res = resbuf[:, 4:]                                      # rows 8 bytes off 16-byte alignment
-    out = f.forward_quantized(qx, sx, epilogue="gate", gate=from_bits(gate, device),
-                              gate_index=torch.from_numpy(gi).to(device), residual=res)
+    gt, git = from_bits(gate, device), torch.from_numpy(gi).to(device)
+    out = f.forward_quantized(qx, sx, epilogue="gate", gate=gt, gate_index=git, residual=res)
+    rc = reference_call(qx, sx, f, "gate", gt, git, res)
     torch.cuda.synchronize()
     want = O.dequant_linear(codes(qx), sx.cpu().numpy().ravel(), codes(f.weight_fp8),
                             f.weight_scale.cpu().numpy().ravel(), epilogue="gate", gate=gate, gate_index=gi,
                             residual=bits(res))
     got = O.bf16_decode(bits(out))
-    assert O.rel_l2(got, want) <= 1e-3 and np.mean(got == want) >= 0.98
+    floor = 0.98
+    if rc is not None:
+        _vs_reference_call(out, rc)
+        same_ref = float(np.mean(O.bf16_decode(bits(rc[0])) == want))
+        floor = same_ref - 4.0 * np.sqrt(max(same_ref * (1.0 - same_ref), 1e-12) / got.size)
+    assert O.rel_l2(got, want) <= 1e-3 and np.mean(got == want) >= floor
 
 
 def test_gemm_single_workload(device):
@@ -364,3 +481,76 @@ def test_gemm_exact_small_integers(device):
     torch.cuda.synchronize()
     want = O.bf16_decode(O.bf16_encode((xi.astype(np.float64) @ wi.T.astype(np.float64)).astype(np.float32)))
     assert np.array_equal(O.bf16_decode(bits(out)), want)
+
+
+def _raw_gemm(f, qx, sx, out, ws=None, epi=0, gate=None, gi=None, grows=0, res=None):
+    """vdn_fp8_gemm (ws None) or vdn_fp8_gemm_ws through the C ABI, into `out`."""
+    import vdn_fp8._lib as L
+    lib = L.load()
+    M, K = qx.shape
+    N = f.weight_fp8.shape[0]
+    st = torch.cuda.current_stream().cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()
+    b = f.bias.detach() if f.bias is not None else None
+    common = (ptr(qx), ptr(sx), ptr(f.weight_fp8), ptr(f.weight_scale), M, N, K, K, K, ptr(b), epi, ptr(gate), ptr(gi),
+              grows, 0 if gate is None else gate.stride(0), ptr(res), 0 if res is None else res.stride(0),
+              ptr(out), N)
+    if ws is None:
+        L.check(lib.vdn_fp8_gemm(*common, st), "gemm")
+    else:
+        L.check(lib.vdn_fp8_gemm_ws(*common, ptr(ws), ws.numel(), st), "gemm_ws")
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(300, 512, 8192, "none"), (1000, 1024, 9216, "gelu_tanh"),
+                                       (777, 768, 8192, "gate_broadcast"), (520, 1032, 8192, "gate_rows"),
+                                       (300, 516, 8192, "gate_rows")])
+def test_gemm_split_k(device, M, N, K, epi):
+    """Shapes whose last round of tiles splits along K (rows of K >= 8192, a last round of at
+    most half the compute units): the units' partial sums go through the workspace and the
+    reduction kernel applies the epilogue. Against the oracle and the reference's own call
+    (as every GEMM), against the unsplit kernel (within one rounding chain: only the order
+    of the binary32 additions differs), and bit-identical from call to call. N = 516 takes
+    the general (unstaged) epilogue in the reduction."""
+    print(f"gemm split-K {epi} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    x, w, b = _rand(rng, (M, K), 1.0), _rand(rng, (N, K), 0.02), _rand(rng, (N,), 0.01)
+    assert vdn_fp8.fp8_linear.gemm_workspace_bytes(M, N, K, device) > 0
+    kw, raw = {}, {}
+    if epi == "gelu_tanh":
+        kw, raw = dict(epilogue="gelu_tanh"), dict(epi=1)
+    elif epi == "gate_broadcast":
+        gate = O.bf16_encode(rng.uniform(0, 2, N).astype(np.float32))
+        kw = dict(epilogue="gate", gate=gate)
+        gt = from_bits(gate, device).reshape(1, N)
+        raw = dict(epi=2, gate=gt, grows=1)
+    elif epi == "gate_rows":
+        T = 3
+        gate = O.bf16_encode(rng.uniform(0, 2, (T, N)).astype(np.float32))
+        gi = rng.integers(0, T, M).astype(np.int32)
+        res = _rand(rng, (M, N), 1.0)
+        kw = dict(epilogue="gate", gate=gate, gate_index=gi, residual=res)
+        raw = dict(epi=2, gate=from_bits(gate, device), gi=torch.from_numpy(gi).to(device), grows=T,
+                   res=from_bits(res, device))
+    _check(x, w, b, device, **kw)
+    f = _linear(w, b, device)
+    qx, sx = vdn_fp8.quantize_rows(from_bits(x, device))
+    ws = torch.empty(vdn_fp8.fp8_linear.gemm_workspace_bytes(M, N, K, device), dtype=torch.uint8, device=device)
+    o_split = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+    o_split2 = torch.empty_like(o_split)
+    o_plain = torch.empty_like(o_split)
+    _raw_gemm(f, qx, sx, o_split, ws, **raw)
+    _raw_gemm(f, qx, sx, o_split2, ws, **raw)
+    _raw_gemm(f, qx, sx, o_plain, None, **raw)
+    torch.cuda.synchronize()
+    assert torch.equal(o_split.view(torch.int16), o_split2.view(torch.int16))
+    d = o_split.float() != o_plain.float()
+    rc = reference_call(qx, sx, f, kw.get("epilogue") or "none",
+                        raw.get("gate"), raw.get("gi"), raw.get("res"))
+    print(f"split vs unsplit: {int(d.sum())} of {d.numel()} outputs differ", flush=True)
+    if rc is not None and int(d.sum()):
+        worst = float(((o_split.float() - o_plain.float()).abs()[d] / (2 * rc[1][d])).max())
+        assert worst <= 1.0, worst
+    # a workspace smaller than the query's answer is refused
+    import vdn_fp8._lib as L
+    with pytest.raises(ValueError, match="workspace"):
+        _raw_gemm(f, qx, sx, o_split, ws[:ws.numel() - 16], **raw)

@@ -52,6 +52,7 @@ constexpr int BN = 256;        // output channels per tile
 constexpr int kThreads = 256;  // 4 wavefronts, 2 (n) x 2 (m), 128 x 128 each
 constexpr int kGroupM = 4;     // m-tiles per group of the tile order (GemmArgs::group_m)
 
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -77,7 +78,35 @@ struct GemmArgs {
     // ((tm + tn) % k_phase_mod) * k_phase_step (mod nk); 0 = no rotation.
     int k_phase_mod, k_phase_step;
     int group_m;   // m-tiles per group of the tile order
+    // Split of the last partial round along K (long rows only): the first t_main tiles
+    // (in tile order) run whole; each of the others runs as `splits` K slices, unit u
+    // being slice u % splits of tile t_main + u / splits, whose fp32 partial sums go to
+    // ws (65536 floats per unit, accumulator layout) and are summed by the reduction
+    // kernel, slice by slice, before the epilogue. units = 0: no split (t_main = T).
+    int t_main, splits, units;
+    float* ws;
 };
+
+constexpr int64_t kUnitFloatsDev = 65536;   // floats of one split unit's partial sums (a 256 x 256 tile)
+
+// Item v of a walk: whole tile v (v < t_main, all K blocks from the tile's rotated
+// start), or split unit v - t_main (blocks [kb0, kb0 + cnt) of its tile, no rotation).
+template <bool PARTIAL>
+__device__ __forceinline__ void gemm_item(const GemmArgs& p, int nk, int v, int& tile, int& kb0, int& cnt, int& unit)
+{
+    if (!PARTIAL) {
+        tile = v; kb0 = -1; cnt = nk; unit = -1;
+    } else {
+        // (integer division runs on the VALU: the results are made scalar again, as the
+        // copies' inline assembly takes the block offset in an SGPR)
+        unit = v - p.t_main;
+        const int r = __builtin_amdgcn_readfirstlane(unit / p.splits);
+        const int sl = unit - r * p.splits;
+        tile = p.t_main + r;
+        kb0 = __builtin_amdgcn_readfirstlane(sl * nk / p.splits);
+        cnt = __builtin_amdgcn_readfirstlane((sl + 1) * nk / p.splits) - kb0;
+    }
+}
 
 // gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3):
 // exp(-2u) = 2^t with t = v (A + B v^2), A = -2 sqrt(2/pi) log2(e), B = 0.044715 A
@@ -250,6 +279,207 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
                    __builtin_amdgcn_readfirstlane((int)bytes), kRsrcWord3};
 }
 
+// Epilogue of the tile at (m0, n0) with its vectors in scalar buffer sb of smem
+// acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4, m = wm*128 +
+// 32 u + lane%32 (tile-relative). Per u and per 64-column half th the wave
+// finishes its 32 x 64 slab in that layout (4 consecutive n per lane),
+// writes it to its staging (32 rows of 128 bytes, padded to 144), reads it
+// back by rows and stores 16-byte pieces of whole 128-byte row segments: lane
+// L covers row 8 i + L/8, channels 8 (L%8) .. +7. The gate and residual
+// apply in that row layout.
+// scal: the tile's vectors (4 KiB: w_scale, x_scale, bias, gate index or gate row, 1 KiB
+// each); stg: this wave's staging rows. Shared by the main kernel and the split-K
+// reduction.
+template <int EPI, bool FAST>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* scal, uint8_t* stg,
+                                              f32x16_t (&acc)[4][4], int64_t m0, int64_t n0, int wave)
+{
+    using namespace mainloop;
+    const int wn = wave & 1, wm = wave >> 1;
+    const bool gate16 = ((p.ldgate & 7) == 0) && (((uintptr_t)p.gate & 15) == 0);
+    const bool res16 = ((p.ldres & 7) == 0) && (((uintptr_t)p.residual & 15) == 0);
+    // Every lane-dependent value here derives from an opaque zero, so the
+    // compiler recomputes it per tile instead of holding it in registers
+    // across the K loop.
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    const int el = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
+    const int frow = el & 31, fh = el >> 5, cc = el & 7, rl = el >> 3;
+    const float* s_sw = reinterpret_cast<const float*>(scal);
+    const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
+    const uint16_t* s_bias = reinterpret_cast<const uint16_t*>(scal + 2048);
+    const int32_t* s_gi = reinterpret_cast<const int32_t*>(scal + 3072);
+    const uint16_t* s_gate = reinterpret_cast<const uint16_t*>(scal + 3072);
+    const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.out + m0 * p.ldo), 0, (int)min(min(p.M - m0, (int64_t)BM) * p.ldo * 2, (int64_t)0x7fffffff), kRsrcWord3);
+    const uint32_t ldo2 = (uint32_t)p.ldo * 2;
+    // Slabs in order (th, u) = (1, 3), (1, 2), .. (0, 0). A column half's per-column
+    // vectors (w_scale, bias and a broadcast gate row, unpacked to binary32) are read
+    // from LDS once and held in registers across its four slabs -- the K loop's
+    // fragment registers are free here. On the fast path the stores trail by one
+    // slab: the previous slab's rows are read back from the staging before this
+    // slab's values overwrite it (a wave's LDS operations run in order), so its
+    // computation hides that read's latency.
+    const bool has_bias = p.bias != nullptr;
+    float hsw[2][4][4], hb[2][4][4], hg[2][4][4];
+    auto hoist = [&](int th) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int nl = wn * 128 + 32 * (2 * th + t2) + 8 * q + 4 * fh;
+                const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
+                hsw[t2][q][0] = sw.x; hsw[t2][q][1] = sw.y; hsw[t2][q][2] = sw.z; hsw[t2][q][3] = sw.w;
+                if (has_bias) {
+                    const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
+                    hb[t2][q][0] = bf16_lo(b.x); hb[t2][q][1] = bf16_hi(b.x);
+                    hb[t2][q][2] = bf16_lo(b.y); hb[t2][q][3] = bf16_hi(b.y);
+                }
+                if (EPI == VDN_FP8_EPI_GATE && FAST) {
+                    const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
+                    hg[t2][q][0] = bf16_lo(gv.x); hg[t2][q][1] = bf16_hi(gv.x);
+                    hg[t2][q][2] = bf16_lo(gv.y); hg[t2][q][3] = bf16_hi(gv.y);
+                }
+            }
+    };
+    // bf16 GEMM output, then the bf16 bias add: each rounding done two values per
+    // conversion, the second one's pairs being the stored words (opaque, so the
+    // compiler keeps the pairs); one uniform branch per slab
+    auto compute = [&](int th, int u, auto with_bias) {
+        const float sxm = s_sx[wm * 128 + 32 * u + frow];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int t = 2 * th + t2;
+                const float* sw = hsw[t2][q];
+                // A rounding to bf16 that the bias add or GELU reads is one conversion per
+                // value (round_bf16_hi: no unpacking); the last one converts the stored
+                // pairs. The gate kernels keep the packed pairs and unpack them (one value
+                // per conversion there made the compiler spill).
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[t][u][4 * q + e] * (sxm * sw[e]);
+                uint32_t r01, r23;
+                if (EPI != VDN_FP8_EPI_GATE) {
+                    if (decltype(with_bias)::value) {
+                        const float* bb = hb[t2][q];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = round_bf16_hi(v[e]) + bb[e];
+                    }
+                    if (EPI == VDN_FP8_EPI_GELU_TANH) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(round_bf16_hi(v[e]));   // of the bf16 output
+                    }
+                    r01 = pack_bf16x2(v[0], v[1]);
+                    r23 = pack_bf16x2(v[2], v[3]);
+                    asm volatile("" : "+v"(r01), "+v"(r23));
+                } else {
+                    r01 = pack_bf16x2(v[0], v[1]);
+                    r23 = pack_bf16x2(v[2], v[3]);
+                    asm volatile("" : "+v"(r01), "+v"(r23));
+                    if (decltype(with_bias)::value) {
+                        const float* bb = hb[t2][q];
+                        r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
+                        r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
+                        asm volatile("" : "+v"(r01), "+v"(r23));
+                    }
+                    if (FAST) {   // broadcast gate row, no residual
+                        const float* gg = hg[t2][q];
+                        r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
+                        r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
+                    }
+                }
+                *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
+            }
+        // these accumulators start the next tile from zero
+        acc[2 * th][u] = f32x16_t{};
+        acc[2 * th + 1][u] = f32x16_t{};
+    };
+    // fast path: the slab's rows 8 i + L/8 from the staging, then their stores (byte
+    // offset of the row, or out of range past N)
+    uint4 pv[4];
+    auto read_slab = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] = *reinterpret_cast<const uint4*>(stg + (8 * i + rl) * kStgRow + (cc << 4));
+    };
+    // (the four offsets first, then the four stores back to back and their wait states)
+    auto store_slab = [&](int th, int u) {
+        const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
+        const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
+        uint32_t off[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) off[i] = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off[i], 0, kStoreNT);
+        settle_stores();
+    };
+#pragma unroll
+    for (int sidx = 0; sidx < 8; ++sidx) {
+        const int th = 1 - sidx / 4, u = 3 - sidx % 4;
+        if (sidx % 4 == 0) hoist(th);
+        if (FAST && sidx > 0) read_slab();   // the previous slab, before this one overwrites it
+        if (has_bias) compute(th, u, std::true_type{});
+        else compute(th, u, std::false_type{});
+        if (FAST) {
+            if (sidx > 0) store_slab(1 - (sidx - 1) / 4, 3 - (sidx - 1) % 4);
+        } else {
+            const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
+            const bool full = n + 8 <= p.N;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 8 * i + rl;
+                uint4 v = *reinterpret_cast<const uint4*>(stg + r * kStgRow + (cc << 4));
+                const int ml = wm * 128 + 32 * u + r;
+                const int64_t m = m0 + ml;
+                if (m >= p.M || n >= p.N) continue;
+                if (EPI == VDN_FP8_EPI_GATE) {
+                    const int64_t gi = p.gate_index ? min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1) : 0;
+                    const uint16_t* gp = p.gate + gi * p.ldgate + n;
+                    uint4 g;
+                    if (gate16 && full) g = *reinterpret_cast<const uint4*>(gp);
+                    else {
+                        const uint2 g0 = *reinterpret_cast<const uint2*>(gp);
+                        const uint2 g1 = full ? *reinterpret_cast<const uint2*>(gp + 4) : make_uint2(0u, 0u);
+                        g = make_uint4(g0.x, g0.y, g1.x, g1.y);
+                    }
+                    uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+                    if (p.residual) {
+                        const uint16_t* rp = p.residual + m * p.ldres + n;
+                        if (res16 && full) rv = *reinterpret_cast<const uint4*>(rp);
+                        else {
+                            const uint2 r0 = *reinterpret_cast<const uint2*>(rp);
+                            const uint2 r1 = full ? *reinterpret_cast<const uint2*>(rp + 4) : make_uint2(0u, 0u);
+                            rv = make_uint4(r0.x, r0.y, r1.x, r1.y);
+                        }
+                    }
+                    const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w},
+                                   rw[4] = {rv.x, rv.y, rv.z, rv.w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float lo = bf16_lo(vw[e]) * bf16_lo(gw[e]), hi = bf16_hi(vw[e]) * bf16_hi(gw[e]);
+                        if (p.residual) { lo += bf16_lo(rw[e]); hi += bf16_hi(rw[e]); }
+                        o[e] = pack_bf16x2(lo, hi);
+                    }
+                    v = make_uint4(o[0], o[1], o[2], o[3]);
+                }
+                uint16_t* dst = p.out + m * p.ldo + n;
+                *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+                if (full) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+            }
+        }
+        // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (FAST) {   // the last slab (th 0, u 0)
+        read_slab();
+        store_slab(0, 0);
+    }
+}
+
 // One workgroup per CU walks tiles blockIdx.x, + gridDim.x, ... The copies form
 // one stream of 128-byte K blocks across those tiles, so the next tile's first
 // two blocks are in flight while this tile's epilogue runs. Per block g (stage
@@ -271,7 +501,10 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // (dropped), so the waits that follow count them and the stores drain while
 // the next tile runs. Otherwise the waits also cover the epilogue's memory
 // operations.
-template <int EPI, bool FAST>
+// PARTIAL: the split units instead of the whole tiles (one per workgroup, its K slice,
+// the partial sums stored raw; a launch of its own, so that the whole-tile kernel keeps
+// one straight-line epilogue; EPI and FAST do not matter to it: one instance serves).
+template <int EPI, bool FAST, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm_fp8(GemmArgs p)
 {
@@ -282,9 +515,10 @@ void k_gemm_fp8(GemmArgs p)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
-    const int T = p.tiles_m * p.tiles_n;
     const int nk = (int)(p.K / BK);
     const int stride = gridDim.x;
+    const int v_begin = PARTIAL ? p.t_main : 0;
+    const int n_items = PARTIAL ? p.t_main + p.units : p.t_main;
 
     // Copies: this wave fills rows 64 wave .. 64 wave + 63 of each tile, 8 rows
     // (1 KiB) per copy. Lane L lands at row +L/8, physical chunk L%8, so it
@@ -299,20 +533,23 @@ void k_gemm_fp8(GemmArgs p)
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
 
-    // Producer: the next block to copy is block pj of tile ptile. Blocks of
-    // tiles past the end still issue their copies, through empty descriptors
-    // (zeros, no memory read), so the vmcnt bookkeeping stays fixed.
-    int ptile = blockIdx.x, pj = 0, pphase = 0, pkb = 0;
+    // Producer: the next block to copy is block pj of item pv (pnk blocks from block
+    // pphase, wrapping). Blocks of items past the end still issue their copies, through
+    // empty descriptors (zeros, no memory read), so the vmcnt bookkeeping stays fixed.
+    int pv = v_begin + blockIdx.x, pj = 0, pphase = 0, pkb = 0, pnk = nk;
     i32x4_t xr, wr;
     auto producer_tile = [&]() {
         int64_t xb = 0, wb = 0;
         const uint8_t* xa = p.xq;
         const uint8_t* wa = p.wq;
         pphase = 0;
-        if (ptile < T) {
-            int tm, tn;
-            tile_coords(ptile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-            if (p.k_phase_mod > 0) pphase = (((tm + tn) % p.k_phase_mod) * p.k_phase_step) % nk;
+        pnk = nk;
+        if (pv < n_items) {
+            int tile, kb0, unit, tm, tn;
+            gemm_item<PARTIAL>(p, nk, pv, tile, kb0, pnk, unit);
+            tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+            if (kb0 >= 0) pphase = kb0;
+            else if (p.k_phase_mod > 0) pphase = (((tm + tn) % p.k_phase_mod) * p.k_phase_step) % nk;
             const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
             xa += m0 * p.ldx;
             wa += n0 * p.ldw;
@@ -334,9 +571,9 @@ void k_gemm_fp8(GemmArgs p)
         else copy16_to_lds(wr, dst + BM * BK + (64 * wave + 8 * i) * BK, woff[i], kb);
     };
     auto advance = [&]() {
-        if (++pj == nk) {
+        if (++pj == pnk) {
             pj = 0;
-            ptile += stride;
+            pv += stride;
             producer_tile();
         } else {
             const int kbi = pj + pphase;
@@ -350,7 +587,7 @@ void k_gemm_fp8(GemmArgs p)
     auto scal_copy = [&](int t, int buf) {
         const void* base = p.sx;
         int64_t bytes = 0;
-        if (t < T) {
+        if (t < p.t_main) {   // whole tiles only (split units store raw partial sums)
             int tm, tn;
             tile_coords(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
             const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -393,204 +630,13 @@ void k_gemm_fp8(GemmArgs p)
     };
     auto fence = [&]() { __builtin_amdgcn_sched_barrier(0); };
 
-    // Epilogue of the tile at (m0, n0) with its vectors in scalar buffer sb.
-    // acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4, m = wm*128 +
-    // 32 u + lane%32 (tile-relative). Per u and per 64-column half th the wave
-    // finishes its 32 x 64 slab in that layout (4 consecutive n per lane),
-    // writes it to its staging (32 rows of 128 bytes, padded to 144), reads it
-    // back by rows and stores 16-byte pieces of whole 128-byte row segments: lane
-    // L covers row 8 i + L/8, channels 8 (L%8) .. +7. The gate and residual
-    // apply in that row layout.
-    const bool gate16 = ((p.ldgate & 7) == 0) && (((uintptr_t)p.gate & 15) == 0);
-    const bool res16 = ((p.ldres & 7) == 0) && (((uintptr_t)p.residual & 15) == 0);
     auto epilogue = [&](int64_t m0, int64_t n0, int sb) {
-        // Every lane-dependent value here derives from an opaque zero, so the
-        // compiler recomputes it per tile instead of holding it in registers
-        // across the K loop.
-        uint32_t zero;
-        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-        const int el = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
-        const int frow = el & 31, fh = el >> 5, cc = el & 7, rl = el >> 3;
-        const uint8_t* scal = smem + kScal + sb * 4096;
-        const float* s_sw = reinterpret_cast<const float*>(scal);
-        const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
-        const uint16_t* s_bias = reinterpret_cast<const uint16_t*>(scal + 2048);
-        const int32_t* s_gi = reinterpret_cast<const int32_t*>(scal + 3072);
-        const uint16_t* s_gate = reinterpret_cast<const uint16_t*>(scal + 3072);
-        uint8_t* const stg = smem + kStg + wave * kStgWave;
-        const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.out + m0 * p.ldo), 0, (int)min(min(p.M - m0, (int64_t)BM) * p.ldo * 2, (int64_t)0x7fffffff), kRsrcWord3);
-        const uint32_t ldo2 = (uint32_t)p.ldo * 2;
-        // Slabs in order (th, u) = (1, 3), (1, 2), .. (0, 0). A column half's per-column
-        // vectors (w_scale, bias and a broadcast gate row, unpacked to binary32) are read
-        // from LDS once and held in registers across its four slabs -- the K loop's
-        // fragment registers are free here. On the fast path the stores trail by one
-        // slab: the previous slab's rows are read back from the staging before this
-        // slab's values overwrite it (a wave's LDS operations run in order), so its
-        // computation hides that read's latency.
-        const bool has_bias = p.bias != nullptr;
-        float hsw[2][4][4], hb[2][4][4], hg[2][4][4];
-        auto hoist = [&](int th) {
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int nl = wn * 128 + 32 * (2 * th + t2) + 8 * q + 4 * fh;
-                    const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
-                    hsw[t2][q][0] = sw.x; hsw[t2][q][1] = sw.y; hsw[t2][q][2] = sw.z; hsw[t2][q][3] = sw.w;
-                    if (has_bias) {
-                        const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
-                        hb[t2][q][0] = bf16_lo(b.x); hb[t2][q][1] = bf16_hi(b.x);
-                        hb[t2][q][2] = bf16_lo(b.y); hb[t2][q][3] = bf16_hi(b.y);
-                    }
-                    if (EPI == VDN_FP8_EPI_GATE && FAST) {
-                        const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
-                        hg[t2][q][0] = bf16_lo(gv.x); hg[t2][q][1] = bf16_hi(gv.x);
-                        hg[t2][q][2] = bf16_lo(gv.y); hg[t2][q][3] = bf16_hi(gv.y);
-                    }
-                }
-        };
-        // bf16 GEMM output, then the bf16 bias add: each rounding done two values per
-        // conversion, the second one's pairs being the stored words (opaque, so the
-        // compiler keeps the pairs); one uniform branch per slab
-        auto compute = [&](int th, int u, auto with_bias) {
-            const float sxm = s_sx[wm * 128 + 32 * u + frow];
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int t = 2 * th + t2;
-                    const float* sw = hsw[t2][q];
-                    // A rounding to bf16 that the bias add or GELU reads is one conversion per
-                    // value (round_bf16_hi: no unpacking); the last one converts the stored
-                    // pairs. The gate kernels keep the packed pairs and unpack them (one value
-                    // per conversion there made the compiler spill).
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = acc[t][u][4 * q + e] * (sxm * sw[e]);
-                    uint32_t r01, r23;
-                    if (EPI != VDN_FP8_EPI_GATE) {
-                        if (decltype(with_bias)::value) {
-                            const float* bb = hb[t2][q];
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = round_bf16_hi(v[e]) + bb[e];
-                        }
-                        if (EPI == VDN_FP8_EPI_GELU_TANH) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(round_bf16_hi(v[e]));   // of the bf16 output
-                        }
-                        r01 = pack_bf16x2(v[0], v[1]);
-                        r23 = pack_bf16x2(v[2], v[3]);
-                        asm volatile("" : "+v"(r01), "+v"(r23));
-                    } else {
-                        r01 = pack_bf16x2(v[0], v[1]);
-                        r23 = pack_bf16x2(v[2], v[3]);
-                        asm volatile("" : "+v"(r01), "+v"(r23));
-                        if (decltype(with_bias)::value) {
-                            const float* bb = hb[t2][q];
-                            r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
-                            r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
-                            asm volatile("" : "+v"(r01), "+v"(r23));
-                        }
-                        if (FAST) {   // broadcast gate row, no residual
-                            const float* gg = hg[t2][q];
-                            r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
-                            r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
-                        }
-                    }
-                    *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
-                }
-            // these accumulators start the next tile from zero
-            acc[2 * th][u] = f32x16_t{};
-            acc[2 * th + 1][u] = f32x16_t{};
-        };
-        // fast path: the slab's rows 8 i + L/8 from the staging, then their stores (byte
-        // offset of the row, or out of range past N)
-        uint4 pv[4];
-        auto read_slab = [&]() {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = *reinterpret_cast<const uint4*>(stg + (8 * i + rl) * kStgRow + (cc << 4));
-        };
-        // (the four offsets first, then the four stores back to back and their wait states)
-        auto store_slab = [&](int th, int u) {
-            const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
-            const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
-            uint32_t off[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) off[i] = n < p.N ? off0 + (uint32_t)(8 * i) * ldo2 : 0x80000000u;
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off[i], 0, kStoreNT);
-            settle_stores();
-        };
-#pragma unroll
-        for (int sidx = 0; sidx < 8; ++sidx) {
-            const int th = 1 - sidx / 4, u = 3 - sidx % 4;
-            if (sidx % 4 == 0) hoist(th);
-            if (FAST && sidx > 0) read_slab();   // the previous slab, before this one overwrites it
-            if (has_bias) compute(th, u, std::true_type{});
-            else compute(th, u, std::false_type{});
-            if (FAST) {
-                if (sidx > 0) store_slab(1 - (sidx - 1) / 4, 3 - (sidx - 1) % 4);
-            } else {
-                const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
-                const bool full = n + 8 <= p.N;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 8 * i + rl;
-                    uint4 v = *reinterpret_cast<const uint4*>(stg + r * kStgRow + (cc << 4));
-                    const int ml = wm * 128 + 32 * u + r;
-                    const int64_t m = m0 + ml;
-                    if (m >= p.M || n >= p.N) continue;
-                    if (EPI == VDN_FP8_EPI_GATE) {
-                        const int64_t gi = p.gate_index ? min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1) : 0;
-                        const uint16_t* gp = p.gate + gi * p.ldgate + n;
-                        uint4 g;
-                        if (gate16 && full) g = *reinterpret_cast<const uint4*>(gp);
-                        else {
-                            const uint2 g0 = *reinterpret_cast<const uint2*>(gp);
-                            const uint2 g1 = full ? *reinterpret_cast<const uint2*>(gp + 4) : make_uint2(0u, 0u);
-                            g = make_uint4(g0.x, g0.y, g1.x, g1.y);
-                        }
-                        uint4 rv = make_uint4(0u, 0u, 0u, 0u);
-                        if (p.residual) {
-                            const uint16_t* rp = p.residual + m * p.ldres + n;
-                            if (res16 && full) rv = *reinterpret_cast<const uint4*>(rp);
-                            else {
-                                const uint2 r0 = *reinterpret_cast<const uint2*>(rp);
-                                const uint2 r1 = full ? *reinterpret_cast<const uint2*>(rp + 4) : make_uint2(0u, 0u);
-                                rv = make_uint4(r0.x, r0.y, r1.x, r1.y);
-                            }
-                        }
-                        const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {g.x, g.y, g.z, g.w},
-                                       rw[4] = {rv.x, rv.y, rv.z, rv.w};
-                        uint32_t o[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            float lo = bf16_lo(vw[e]) * bf16_lo(gw[e]), hi = bf16_hi(vw[e]) * bf16_hi(gw[e]);
-                            if (p.residual) { lo += bf16_lo(rw[e]); hi += bf16_hi(rw[e]); }
-                            o[e] = pack_bf16x2(lo, hi);
-                        }
-                        v = make_uint4(o[0], o[1], o[2], o[3]);
-                    }
-                    uint16_t* dst = p.out + m * p.ldo + n;
-                    *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
-                    if (full) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
-                }
-            }
-            // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (FAST) {   // the last slab (th 0, u 0)
-            read_slab();
-            store_slab(0, 0);
-        }
+        tile_epilogue<EPI, FAST>(p, smem + kScal + sb * 4096, smem + kStg + wave * kStgWave, acc, m0, n0, wave);
     };
 
     // Prologue: the first tile's vectors, then blocks 0 and 1 of the stream.
     producer_tile();
-    scal_copy(blockIdx.x, 0);
+    scal_copy(v_begin + blockIdx.x, 0);
     // W copies (c = 8..15) before X copies (c = 0..7), as in the loop
 #pragma unroll
     for (int c = 0; c < kBlockCopies; ++c) copy(0, (c + kCopies) % kBlockCopies);
@@ -606,21 +652,22 @@ void k_gemm_fp8(GemmArgs p)
         for (int u = 0; u < 4; ++u) acc[t][u] = f32x16_t{};   // the epilogue re-zeroes them per tile
     int g = 0;    // stream index of the block being computed
     int k = 0;    // tiles done by this workgroup
-    for (int tile = blockIdx.x; tile < T; tile += stride, ++k) {
-        int tm, tn;
+    for (int v = v_begin + blockIdx.x; v < n_items; v += stride, ++k) {
+        int tile, kb0, cnt, unit, tm, tn;
+        gemm_item<PARTIAL>(p, nk, v, tile, kb0, cnt, unit);
         tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
         // Block g has landed once only block g+1's copies -- and, after the first
         // tile, the previous epilogue's stores -- may be pending.
         if (k == 0) wave_sync<kBlockCopies>();
         else wave_sync<kBlockCopies + kE>();
-        scal_copy(tile + stride, (k + 1) & 1);   // every wave is past the epilogue that used that buffer
+        scal_copy(v + stride, (k + 1) & 1);   // every wave is past the epilogue that used that buffer
 #pragma unroll
         for (int f = 0; f < 8; ++f) read_into(g & 1, 0, f, w0, x0);
 
-        for (int j = 0; j < nk; ++j, ++g) {
+        for (int j = 0; j < cnt; ++j, ++g) {
             const int st = g & 1;
-            const bool more = j + 1 < nk;
+            const bool more = j + 1 < cnt;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 mfma(w0, x0, q);
@@ -657,10 +704,113 @@ void k_gemm_fp8(GemmArgs p)
                 fence();
             }
         }
-        epilogue(m0, n0, k & 1);
+        if constexpr (!PARTIAL) {
+            epilogue(m0, n0, k & 1);
+        } else {
+            // A split unit stores its partial sums in accumulator layout: float4 r4 of accumulator (t, u)
+            // of lane L at ((wave * 16 + 4 t + u) * 4 + r4) * 256 + 4 L of the unit's
+            // 65536 floats, one whole KiB per wave store.
+            // (a buffer descriptor over the wave's 64 KiB, one accumulator's four stores at a
+            // time: the 256 accumulators are not all moved to VGPRs at once)
+            const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(p.ws + ((int64_t)unit * 4 + wave) * 16384), 0, 65536, kRsrcWord3);
+            uint32_t zero;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+            const uint32_t l16 = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero) * 16;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(i32x4_t, f32x4_t{acc[t][u][4 * r4], acc[t][u][4 * r4 + 1],
+                                                                acc[t][u][4 * r4 + 2], acc[t][u][4 * r4 + 3]}),
+                            wsr, l16, ((4 * t + u) * 4 + r4) * 1024, 0);
+                    settle_stores();
+                }
+        }
     }
     // No copy may still be writing LDS when the workgroup ends.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+}
+
+// Split-K reduction: one single-wave workgroup per quadrant of a split tile (four per
+// tile, one wave per SIMD). The wave sums its accumulators' partial sums over the tile's
+// units in slice order (slice 0 + slice 1 + ..., binary32: the order depends only on K and
+// the split), each slice's 64 KiB read by 64 loads in flight at once, stages the tile's
+// vectors as the main kernel's copies lay them out, and runs the same epilogue for its
+// quadrant.
+template <int EPI, bool FAST>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemm_splitk_reduce(GemmArgs p)
+{
+    using namespace mainloop;
+    __shared__ __attribute__((aligned(1024))) uint8_t scal[4096];
+    __shared__ __attribute__((aligned(16))) uint8_t stg[kStgWave];
+    const int lane = threadIdx.x;
+    const int quad = blockIdx.x & 3, r = blockIdx.x >> 2;
+    int tm, tn;
+    tile_coords(p.t_main + r, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    // (branch-free buffer loads, all in flight at once: entries past N or M read as zeros)
+    {
+        const int64_t nn = min(p.N - n0, (int64_t)256), mm = min(p.M - m0, (int64_t)256);
+        const __amdgpu_buffer_rsrc_t swr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sw + n0), 0, (int)(nn * 4), kRsrcWord3);
+        const __amdgpu_buffer_rsrc_t sxr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sx + m0), 0, (int)(mm * 4), kRsrcWord3);
+        const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.bias ? p.bias + n0 : nullptr), 0, p.bias ? (int)(nn * 2) : 0, kRsrcWord3);
+        const bool grow = EPI == VDN_FP8_EPI_GATE && FAST;
+        const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+            grow ? (void*)(p.gate + n0) : (void*)(p.gate_index ? p.gate_index + m0 : nullptr), 0,
+            grow ? (int)(nn * 2) : (p.gate_index ? (int)(mm * 4) : 0), kRsrcWord3);
+        const uint32_t l16 = (uint32_t)lane * 16, l8 = (uint32_t)lane * 8;
+        const i32x4_t vsw = __builtin_amdgcn_raw_buffer_load_b128(swr, l16, 0, 0);
+        const i32x4_t vsx = __builtin_amdgcn_raw_buffer_load_b128(sxr, l16, 0, 0);
+        const i32x2_t vb = __builtin_amdgcn_raw_buffer_load_b64(br, l8, 0, 0);
+        const i32x4_t vg4 = grow ? i32x4_t{} : __builtin_amdgcn_raw_buffer_load_b128(gr, l16, 0, 0);
+        const i32x2_t vg2 = grow ? __builtin_amdgcn_raw_buffer_load_b64(gr, l8, 0, 0) : i32x2_t{};
+        *reinterpret_cast<i32x4_t*>(scal + l16) = vsw;
+        *reinterpret_cast<i32x4_t*>(scal + 1024 + l16) = vsx;
+        *reinterpret_cast<i32x2_t*>(scal + 2048 + l8) = vb;
+        if (grow) *reinterpret_cast<i32x2_t*>(scal + 3072 + l8) = vg2;
+        else *reinterpret_cast<i32x4_t*>(scal + 3072 + l16) = vg4;
+    }
+    const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.ws + (int64_t)r * p.splits * kUnitFloatsDev + (int64_t)quad * 16384), 0,
+        (int)min((int64_t)p.splits * kUnitFloatsDev * 4, (int64_t)0x7fffffff), kRsrcWord3);
+    const uint32_t l16 = (uint32_t)lane * 16;
+    // (the later slices in batches of 32 loads, each batch in flight at once: the
+    // registers hold the sums and one batch)
+    f32x4_t a[64], b[32];
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+        a[i] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, i * 1024, 0));
+    for (int sl = 1; sl < p.splits; ++sl) {
+        const int so = sl * (int)kUnitFloatsDev * 4;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                b[i] = __builtin_bit_cast(f32x4_t,
+                                          __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, so + (32 * c + i) * 1024, 0));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) a[32 * c + i] += b[i];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    f32x16_t acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][u][4 * r4 + e] = a[(4 * t + u) * 4 + r4][e];
+    __syncthreads();
+    tile_epilogue<EPI, FAST>(p, scal, stg, acc, m0, n0, quad);
 }
 
 // ---------------------------------------------------------------------------
@@ -779,22 +929,60 @@ __host__ inline void tile_order(int64_t N, int64_t K, int& phase_mod, int& group
     if (N <= 6144 && K >= 8192) group_m = 2;
 }
 
-// Compute units of the current device (the persistent kernel's grid), cached per
-// device; 0 if the runtime cannot say.
+// Split of the last partial round along K: for rows of at least 8192 bytes (K), when
+// the tiles leave a last round of R <= grid / 2 tiles, each of those R tiles runs as S =
+// min(grid / R, nk / 8) K slices on otherwise idle workgroups (at least 8 blocks each),
+// then the reduction kernel sums the slices. The H3 FF down projection [13107, 5376,
+// 14336]: 1092 tiles = 4 rounds + 68 on 256 CUs, the 68 as 3 slices of 37-38 blocks.
+// Projections with shorter rows (the QKV and FF projections) never split, so a fused
+// weight's outputs keep the bits of its separate projections.
+constexpr int64_t kSplitMinK = 8192;
+constexpr int kSplitMinBlocks = 8;
+constexpr int64_t kUnitFloats = 65536;   // one 256 x 256 tile of binary32 partial sums
+
+struct SplitPlan {
+    int t_main, splits, units;
+};
+
+__host__ inline SplitPlan plan_split(int64_t T, int grid, int64_t K)
+{
+    SplitPlan sp{(int)T, 0, 0};
+    if (K < kSplitMinK || K % mainloop::BK || grid <= 0) return sp;
+    const int64_t R = T % grid;
+    if (R == 0 || R > grid / 2) return sp;
+    const int64_t S = std::min<int64_t>(grid / R, K / mainloop::BK / kSplitMinBlocks);
+    if (S < 2) return sp;
+    sp.t_main = (int)(T - R);
+    sp.splits = (int)S;
+    sp.units = (int)(R * S);
+    return sp;
+}
 
 }  // namespace
 
 int launch_gated_residual(const uint16_t* residual, int64_t ldr, const uint16_t* gate, int64_t ldgate,
                           const int32_t* gate_index, int64_t gate_rows, const uint16_t* branch, int64_t ldb,
                           uint16_t* out, int64_t ldo, int64_t M, int64_t N, hipStream_t stream);
-}  // namespace vdn
 
-using namespace vdn;
+// Bytes of split-K workspace a [M, N, K] GEMM takes on the current device (0: no split).
+int gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t* bytes)
+{
+    *bytes = 0;
+    if (M <= 0 || N <= 0 || K <= 0) return VDN_FP8_OK;
+    const int cus = device_cus();
+    if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "gemm: cannot query the device's compute units");
+    const int64_t T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (T > (int64_t)INT32_MAX / 2) return VDN_FP8_OK;
+    const SplitPlan sp = plan_split(T, cus, K);
+    *bytes = (int64_t)sp.units * kUnitFloats * (int64_t)sizeof(float);
+    return VDN_FP8_OK;
+}
 
-extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, int64_t M,
-                            int64_t N, int64_t K, int64_t ldx, int64_t ldw, const void* bias, int epilogue,
-                            const void* gate, const int32_t* gate_index, int64_t gate_rows, int64_t ldgate,
-                            const void* residual, int64_t ldres, void* out, int64_t ldo, hipStream_t stream)
+// The GEMM with an optional split-K workspace (ws NULL: no split).
+int gemm_launch(const void* xq, const float* x_scale, const void* wq, const float* w_scale, int64_t M, int64_t N,
+                int64_t K, int64_t ldx, int64_t ldw, const void* bias, int epilogue, const void* gate,
+                const int32_t* gate_index, int64_t gate_rows, int64_t ldgate, const void* residual, int64_t ldres,
+                void* out, int64_t ldo, float* ws, int64_t ws_bytes, hipStream_t stream)
 {
     if (M < 0 || N < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "gemm: negative shape");
     if (M == 0 || N == 0) return VDN_FP8_OK;
@@ -816,21 +1004,38 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     } else if (epilogue != VDN_FP8_EPI_NONE && epilogue != VDN_FP8_EPI_GELU_TANH) {
         return set_error(VDN_FP8_EINVAL, "gemm: unknown epilogue %d", epilogue);
     }
+    if (ws_bytes < 0 || (ws && !aligned(ws, 16))) return set_error(VDN_FP8_EINVAL, "gemm: workspace must be 16-byte aligned");
     const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     if (tiles_m * tiles_n > (int64_t)INT32_MAX / 2) return set_error(VDN_FP8_EINVAL, "gemm: problem too large");
+    const int64_t T = tiles_m * tiles_n;
     GemmArgs p{(const uint8_t*)xq, x_scale, (const uint8_t*)wq, w_scale, M, N, K, ldx, ldw,
                (const uint16_t*)bias, (const uint16_t*)gate, gate_index, gate_rows, ldgate,
                (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n,
-               kPhaseMod, kPhaseStep, kGroupM};
+               kPhaseMod, kPhaseStep, kGroupM, (int)T, 0, 0, nullptr};
     tile_order(N, K, p.k_phase_mod, p.group_m);
     const bool main = (K % mainloop::BK) == 0;
-    int64_t blocks = tiles_m * tiles_n;
+    int64_t blocks = T;
     if (main) {
         const int cus = device_cus();
         if (cus <= 0) return set_error(VDN_FP8_ELAUNCH, "gemm: cannot query the device's compute units");
-        blocks = std::min<int64_t>(blocks, cus);
+        if (ws) {
+            const SplitPlan sp = plan_split(T, cus, K);
+            const int64_t need = (int64_t)sp.units * kUnitFloats * (int64_t)sizeof(float);
+            if (ws_bytes < need)
+                return set_error(VDN_FP8_EINVAL, "gemm: workspace of %lld bytes, this shape needs %lld",
+                                 (long long)ws_bytes, (long long)need);
+            if (sp.units) {
+                p.t_main = sp.t_main;
+                p.splits = sp.splits;
+                p.units = sp.units;
+                p.ws = ws;
+            }
+        }
+        blocks = std::min<int64_t>((int64_t)p.t_main, cus);
     }
-    const dim3 grid((unsigned)blocks), block(kThreads);
+    const dim3 grid((unsigned)std::max<int64_t>(blocks, 1)), block(kThreads);
+    const dim3 ugrid((unsigned)std::max(p.units, 1)), rgrid((unsigned)(p.units ? 4 * (p.units / p.splits) : 1));
+    const dim3 rblock(64);
     // the fast epilogue: 16-byte output rows, row offsets within 31 bits, and no
     // per-row gate or residual (a gate table of one row is staged like the bias)
     const bool gate_broadcast = epilogue == VDN_FP8_EPI_GATE && !residual && (gate_rows == 1 || !gate_index) &&
@@ -842,17 +1047,33 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     // two roundings as the epilogue, without its per-row loads inside the GEMM.
     if (main && epilogue == VDN_FP8_EPI_GATE && !gate_broadcast && out16 && aligned(gate, 16) && ldgate % 8 == 0 &&
         (!residual || (aligned(residual, 16) && ldres % 8 == 0))) {
-        hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true>), grid, block, 0, stream, p);
+        if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, false>), grid, block, 0, stream, p);
+        if (p.units) {
+            hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
+            hipLaunchKernelGGL((k_gemm_splitk_reduce<VDN_FP8_EPI_NONE, true>), rgrid, rblock, 0, stream, p);
+        }
         const int st = check_launch("gemm");
         if (st != VDN_FP8_OK) return st;
         return launch_gated_residual((const uint16_t*)residual, ldres, (const uint16_t*)gate, ldgate, gate_index,
                                      gate_rows, (const uint16_t*)out, ldo, (uint16_t*)out, ldo, M, N, stream);
     }
-#define VDN_LAUNCH(E)                                                                          \
-    do {                                                                                       \
-        if (main && fast) hipLaunchKernelGGL((k_gemm_fp8<E, true>), grid, block, 0, stream, p);  \
-        else if (main) hipLaunchKernelGGL((k_gemm_fp8<E, false>), grid, block, 0, stream, p);    \
-        else hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);             \
+#define VDN_LAUNCH(E)                                                                                    \
+    do {                                                                                                 \
+        if (main && fast) {                                                                              \
+            if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<E, true, false>), grid, block, 0, stream, p);   \
+            if (p.units) {                                                                               \
+                hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p); \
+                hipLaunchKernelGGL((k_gemm_splitk_reduce<E, true>), rgrid, rblock, 0, stream, p);        \
+            }                                                                                            \
+        } else if (main) {                                                                               \
+            if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<E, false, false>), grid, block, 0, stream, p);  \
+            if (p.units) {                                                                               \
+                hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p); \
+                hipLaunchKernelGGL((k_gemm_splitk_reduce<E, false>), rgrid, rblock, 0, stream, p);       \
+            }                                                                                            \
+        } else {                                                                                         \
+            hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);                        \
+        }                                                                                                \
     } while (0)
     switch (epilogue) {
         case VDN_FP8_EPI_NONE: VDN_LAUNCH(VDN_FP8_EPI_NONE); break;
@@ -861,4 +1082,32 @@ extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq
     }
 #undef VDN_LAUNCH
     return check_launch("gemm");
+}
+}  // namespace vdn
+
+using namespace vdn;
+
+extern "C" int vdn_fp8_gemm(const void* xq, const float* x_scale, const void* wq, const float* w_scale, int64_t M,
+                            int64_t N, int64_t K, int64_t ldx, int64_t ldw, const void* bias, int epilogue,
+                            const void* gate, const int32_t* gate_index, int64_t gate_rows, int64_t ldgate,
+                            const void* residual, int64_t ldres, void* out, int64_t ldo, hipStream_t stream)
+{
+    return gemm_launch(xq, x_scale, wq, w_scale, M, N, K, ldx, ldw, bias, epilogue, gate, gate_index, gate_rows,
+                       ldgate, residual, ldres, out, ldo, nullptr, 0, stream);
+}
+
+extern "C" int vdn_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int64_t* bytes)
+{
+    if (!bytes) return set_error(VDN_FP8_EINVAL, "gemm_workspace_size: null pointer");
+    return gemm_workspace_bytes(M, N, K, bytes);
+}
+
+extern "C" int vdn_fp8_gemm_ws(const void* xq, const float* x_scale, const void* wq, const float* w_scale, int64_t M,
+                               int64_t N, int64_t K, int64_t ldx, int64_t ldw, const void* bias, int epilogue,
+                               const void* gate, const int32_t* gate_index, int64_t gate_rows, int64_t ldgate,
+                               const void* residual, int64_t ldres, void* out, int64_t ldo, void* workspace,
+                               int64_t workspace_bytes, hipStream_t stream)
+{
+    return gemm_launch(xq, x_scale, wq, w_scale, M, N, K, ldx, ldw, bias, epilogue, gate, gate_index, gate_rows,
+                       ldgate, residual, ldres, out, ldo, (float*)workspace, workspace_bytes, stream);
 }

@@ -12,7 +12,7 @@ import os
 
 from .build import CSRC, INCLUDE, LIB_PATH, compiler_id, source_manifest
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, EINVAL, ELAUNCH = 0, 1, 2
 EPI_NONE, EPI_GELU_TANH, EPI_GATE = 0, 1, 2
@@ -30,6 +30,9 @@ EXPORTS = (
     ("vdn_fp8_requantize_weight", _I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _F32, _P, _I64, _P, _P, _P]),
     ("vdn_fp8_gemm", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
                             _P, _I64, _P, _I64, _P]),
+    ("vdn_fp8_gemm_workspace_size", _I32, [_I64, _I64, _I64, _P]),
+    ("vdn_fp8_gemm_ws", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
+                               _P, _I64, _P, _I64, _P, _I64, _P]),
     ("vdn_fp8_qk_prep", _I32, [_P, _I64, _I64, _I64, _I64, _P, _F32, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     ("vdn_fp8_gated_residual", _I32, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P]),
     ("vdn_fp8_last_error", ctypes.c_char_p, []),

@@ -22,6 +22,8 @@ Extensions (keyword-only, additive): `Fp8Linear.forward_quantized` and `forward`
 the GEMM; `Fp8Linear(linear, lora=(A, B, scale))` quantizes W + scale * B @ A in one
 kernel without writing the merged bf16 weight.
 """
+import ctypes
+
 import torch
 import torch.nn as nn
 
@@ -64,6 +66,21 @@ def _rows(x):
     if x.dtype != torch.bfloat16:
         raise ValueError(f"the fp8 quantiser takes bfloat16 input, got {x.dtype}")
     return x.contiguous()
+
+
+_WS_BYTES = {}
+
+
+def gemm_workspace_bytes(M, N, K, device):
+    """Bytes of split-K workspace the GEMM of [M, N, K] takes on `device` (0 for most
+    shapes: only long rows, K >= 8192, whose tiles leave a last round of at most half the
+    compute units split it). The C side allocates nothing: torch provides the buffer."""
+    key = (device.index, M, N, K)
+    if key not in _WS_BYTES:
+        out = ctypes.c_int64(0)
+        _lib.check(_lib.load().vdn_fp8_gemm_workspace_size(M, N, K, ctypes.byref(out)), "gemm_workspace_size")
+        _WS_BYTES[key] = out.value
+    return _WS_BYTES[key]
 
 
 def quantize_rows(x):
@@ -301,10 +318,12 @@ class Fp8Linear(nn.Module):
         elif gate is not None or residual is not None or gate_index is not None:
             raise ValueError('gate / gate_index / residual need epilogue="gate"')
         lib = _lib.load()
-        _lib.check(lib.vdn_fp8_gemm(_ptr(x_fp8), _ptr(x_scale), _ptr(self.weight_fp8),
-                                    _ptr(self.weight_scale), M, N, K, x_fp8.stride(0), K,
-                                    _ptr(bias), epi, _ptr(g), _ptr(gi), grows, ldgate, _ptr(res), ldres,
-                                    _ptr(out), N, _stream(x_fp8)),
+        ws_bytes = gemm_workspace_bytes(M, N, K, dev)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+        _lib.check(lib.vdn_fp8_gemm_ws(_ptr(x_fp8), _ptr(x_scale), _ptr(self.weight_fp8),
+                                       _ptr(self.weight_scale), M, N, K, x_fp8.stride(0), K,
+                                       _ptr(bias), epi, _ptr(g), _ptr(gi), grows, ldgate, _ptr(res), ldres,
+                                       _ptr(out), N, _ptr(ws), ws_bytes, _stream(x_fp8)),
                    "fp8 gemm")
         return out
 
