@@ -184,6 +184,26 @@ int vdn_fp8_gemm_ws(const void *xq, const float *x_scale, const void *wq, const 
                     hipStream_t stream);
 
 /*
+ * vdn_fp8_gemm_ws without the workspace argument and without allocating: a split
+ * shape uses a static 64 MiB device array of the library instead (one per GPU,
+ * held until the process ends; its address is looked up on the first call on
+ * each device). Same kernels, same bits as vdn_fp8_gemm_ws. Shapes whose split
+ * workspace would exceed 64 MiB are refused (EINVAL); on a 256-CU part none
+ * does. Every call on one GPU shares that array and nothing in it needs to start
+ * at zero (each split fully writes its partial sums before they are read), but
+ * two calls that overlap on one GPU (different streams) race on it.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.
+ * Requires: as vdn_fp8_gemm.
+ */
+int vdn_fp8_gemm_noalloc(const void *xq, const float *x_scale, const void *wq, const float *w_scale,
+                         int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                         const void *bias, int epilogue, const void *gate, const int32_t *gate_index,
+                         int64_t gate_rows, int64_t ldgate, const void *residual, int64_t ldres,
+                         void *out, int64_t ldo, hipStream_t stream);
+
+/*
  * QK preparation between the q (or k) projection and attention: per-head
  * RMSNorm, then rotary embedding, in one pass.
  *   rstd   = 1 / sqrt(sum_i x[t][h][i]^2 / d + eps)                (binary32)

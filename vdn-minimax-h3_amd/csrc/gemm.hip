@@ -40,6 +40,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "vdn_common.h"
@@ -1110,4 +1111,57 @@ extern "C" int vdn_fp8_gemm_ws(const void* xq, const float* x_scale, const void*
 {
     return gemm_launch(xq, x_scale, wq, w_scale, M, N, K, ldx, ldw, bias, epilogue, gate, gate_index, gate_rows,
                        ldgate, residual, ldres, out, ldo, (float*)workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The allocation-free GEMM: the split-K workspace in a static device array
+// ---------------------------------------------------------------------------
+// Largest split workspace on a 256-CU part: units <= compute units, 256 KiB each.
+constexpr int64_t kScratchBytes = 64LL << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxScratchDevices];   // this device's copy of `scratch`, or null before the first call
+
+// The device address of `scratch` on the current device, looked up on the first call on
+// each device (the host-side name is not a device address); null if the lookup fails.
+float* scratch_ptr(int dev)
+{
+    if (dev < 0 || dev >= kMaxScratchDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch[dev] = static_cast<float*>(ptr);
+    }
+    return g_scratch[dev];
+}
+}  // namespace
+
+extern "C" int vdn_fp8_gemm_noalloc(const void* xq, const float* x_scale, const void* wq, const float* w_scale,
+                                    int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, const void* bias,
+                                    int epilogue, const void* gate, const int32_t* gate_index, int64_t gate_rows,
+                                    int64_t ldgate, const void* residual, int64_t ldres, void* out, int64_t ldo,
+                                    hipStream_t stream)
+{
+    int64_t need = 0;
+    const int st = gemm_workspace_bytes(M, N, K, &need);
+    if (st != VDN_FP8_OK) return st;
+    if (need > kScratchBytes)
+        return set_error(VDN_FP8_EINVAL, "gemm_noalloc: this shape's split workspace (%lld bytes) exceeds the "
+                                         "static scratch of %lld bytes", (long long)need, (long long)kScratchBytes);
+    float* ws = nullptr;
+    if (need > 0) {
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess) return set_error(VDN_FP8_ELAUNCH, "gemm_noalloc: no current device");
+        ws = scratch_ptr(dev);
+        if (!ws) return set_error(VDN_FP8_ELAUNCH, "gemm_noalloc: cannot look up the scratch array on device %d", dev);
+    }
+    return gemm_launch(xq, x_scale, wq, w_scale, M, N, K, ldx, ldw, bias, epilogue, gate, gate_index, gate_rows,
+                       ldgate, residual, ldres, out, ldo, ws, ws ? kScratchBytes : 0, stream);
 }

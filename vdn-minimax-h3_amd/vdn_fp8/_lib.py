@@ -33,6 +33,8 @@ EXPORTS = (
     ("vdn_fp8_gemm_workspace_size", _I32, [_I64, _I64, _I64, _P]),
     ("vdn_fp8_gemm_ws", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
                                _P, _I64, _P, _I64, _P, _I64, _P]),
+    ("vdn_fp8_gemm_noalloc", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
+                                    _P, _I64, _P, _I64, _P]),
     ("vdn_fp8_qk_prep", _I32, [_P, _I64, _I64, _I64, _I64, _P, _F32, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     ("vdn_fp8_gated_residual", _I32, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P]),
     ("vdn_fp8_last_error", ctypes.c_char_p, []),
