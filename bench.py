@@ -390,11 +390,12 @@ def _only(name, steps, warmup):
     elif name == "swiglu_h3":
         h = torch.empty(wl.TOKENS, 2 * 14336, dtype=torch.bfloat16, device=dev).normal_()
         fn = lambda: vdn_fp8.swiglu_quantize(h)
-    elif name == "pre_norm_quantize":
-        x = torch.empty(wl.TOKENS, wl.HIDDEN, dtype=torch.bfloat16, device=dev).normal_()
-        nw = torch.ones(wl.HIDDEN, dtype=torch.bfloat16, device=dev)
-        tab = (0.2 * torch.randn(21, wl.HIDDEN, device=dev)).to(torch.bfloat16)
-        idx = (torch.arange(wl.TOKENS, device=dev) * 21 // wl.TOKENS).to(torch.int32)
+    elif name in ("pre_norm_quantize", "pre_norm_quantize_h3"):
+        M_, K_, T_ = (wl.TOKENS, wl.HIDDEN, 21) if name == "pre_norm_quantize" else (13107, 5376, 5)
+        x = torch.empty(M_, K_, dtype=torch.bfloat16, device=dev).normal_()
+        nw = torch.ones(K_, dtype=torch.bfloat16, device=dev)
+        tab = (0.2 * torch.randn(T_, K_, device=dev)).to(torch.bfloat16)
+        idx = (torch.arange(M_, device=dev) * T_ // M_).to(torch.int32)
         fn = lambda: FB.pre_quantize(x, nw, 1e-6, tab, tab, idx)
     elif name == "post":
         x = torch.empty(wl.TOKENS, wl.HIDDEN, dtype=torch.bfloat16, device=dev).normal_()
@@ -433,7 +434,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time one workload's kernel alone (lora_requant, requant, "
-                    "quantize_5120, quantize_13824, swiglu_h3, pre_norm_quantize, post, qk_prep, gemm_h3_ff_down, "
+                    "quantize_5120, quantize_13824, swiglu_h3, pre_norm_quantize, pre_norm_quantize_h3, post, qk_prep, "
+                    "gemm_h3_ff_down, "
                     "gemm_qkv)")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -517,10 +517,11 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 // 16-byte reads cover consecutive addresses.
 // Waves per workgroup: three per SIMD while the two row buffers leave room (168
 // VGPRs), two for rows of more than 512 chunks -- except with the table (the affine
-// form) at 640 chunks, where twelve fit once the next row's loads go out after the
-// row's normalization instead of before (0.0880 against 0.0907 ms with eight waves
-// and the early loads).
-constexpr int norm_row_waves(int cpl, bool affine) { return cpl <= 8 || (cpl == 10 && affine) ? 12 : 8; }
+// form) at 640 and 704 chunks, where twelve fit once the next row's loads go out after
+// the row's normalization instead of before (0.0880 against 0.0907 ms with eight waves
+// and the early loads at 640; H3's 5376-wide rows, 672 chunks, as 11 per lane:
+// [13107, 5376] 0.0428 against 0.0471 ms with eight waves and 12 per lane).
+constexpr int norm_row_waves(int cpl, bool affine) { return cpl <= 8 || ((cpl == 10 || cpl == 11) && affine) ? 12 : 8; }
 constexpr bool norm_row_late_load(int cpl, bool affine) { return cpl > 8 && norm_row_waves(cpl, affine) == 12; }
 // Rows in flight per wave besides the one computed (two, in the registers two waves
 // per SIMD leave at 64 chunks x 10, measured 0.0911 ms against 0.0891 ms with one).
@@ -920,6 +921,7 @@ void launch_norm_rows(int64_t nch, int64_t M, const NormArgs& p, int cus, hipStr
     if (nch <= 6 * kLanes) go(std::integral_constant<int, 6>{});
     else if (nch <= 8 * kLanes) go(std::integral_constant<int, 8>{});
     else if (nch <= 10 * kLanes) go(std::integral_constant<int, 10>{});
+    else if (nch <= 11 * kLanes) go(std::integral_constant<int, 11>{});   // H3's 5376
     else if (nch <= 12 * kLanes) go(std::integral_constant<int, 12>{});
     else go(std::integral_constant<int, 14>{});
 }
