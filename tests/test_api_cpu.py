@@ -173,3 +173,35 @@ def test_swiglu_one_rounding_against_float64():
     same, same_eager = np.mean(got == want), np.mean(eager == want)
     assert same >= 0.995, same
     assert same_eager < same, (same_eager, same)
+
+
+def test_host_linear_needs_a_gpu_here():
+    """Fp8Linear of a host-resident Linear is requantized on the GPU and its buffers return
+    to the Linear's device; without a GPU it raises (no CPU fallback)."""
+    import torch
+    import vdn_fp8
+    if torch.cuda.is_available():
+        pytest.skip("this container's check: no GPU")
+    lin = torch.nn.Linear(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="needs a GPU"):
+        vdn_fp8.Fp8Linear(lin)
+
+
+def test_index_checks_opt_in():
+    """Out-of-range table indices are clamped by the kernels; with checks enabled the host
+    raises IndexError first, as the reference's index_select does."""
+    import torch
+    import vdn_fp8
+    from vdn_fp8.fp8_linear import check_index_range
+    idx = torch.tensor([0, 3, 5])
+    prev = vdn_fp8.set_index_checks(False)
+    try:
+        check_index_range(idx, 5, "gate_index")            # off: no check
+        vdn_fp8.set_index_checks(True)
+        check_index_range(torch.tensor([0, 4]), 5, "gate_index")
+        with pytest.raises(IndexError, match="out of range"):
+            check_index_range(idx, 5, "gate_index")
+        with pytest.raises(IndexError):
+            check_index_range(torch.tensor([-1]), 5, "indices")
+    finally:
+        vdn_fp8.set_index_checks(prev)

@@ -91,3 +91,55 @@ def test_merge_lora_and_convert_equals_merge_then_convert(device, rank, scale):
             assert torch.equal(ma.weight_scale, mb.weight_scale), na
         elif isinstance(ma, nn.Linear):
             assert torch.equal(ma.weight, mb.weight), na      # pairs on kept-bf16 Linears merged in place
+
+
+def test_host_resident_linear(device):
+    """A Linear still in host memory: requantized on the GPU, buffers returned to the
+    host (where the reference's eager branch would leave them), identical to the GPU-built
+    module's; moved to the GPU, it runs as usual."""
+    torch.manual_seed(3)
+    lin = torch.nn.Linear(512, 256, dtype=torch.bfloat16)
+    f_host = vdn_fp8.Fp8Linear(lin)
+    assert f_host.weight_fp8.device.type == "cpu" and f_host.weight_scale.device.type == "cpu"
+    f_dev = vdn_fp8.Fp8Linear(_copy_to(lin, device))
+    assert torch.equal(f_host.weight_fp8.view(torch.uint8), f_dev.weight_fp8.view(torch.uint8).cpu())
+    assert torch.equal(f_host.weight_scale, f_dev.weight_scale.cpu())
+    f_host = f_host.to(device)
+    x = torch.randn(64, 512, dtype=torch.bfloat16, device=device)
+    assert torch.equal(f_host(x).view(torch.int16), f_dev(x).view(torch.int16))
+
+
+def _copy_to(lin, device):
+    out = torch.nn.Linear(lin.in_features, lin.out_features, dtype=torch.bfloat16, device=device)
+    with torch.no_grad():
+        out.weight.copy_(lin.weight)
+        out.bias.copy_(lin.bias)
+    return out
+
+
+def test_index_checks_raise_before_launch(device):
+    """With index checks on, an out-of-range gate or modulation index raises IndexError (as
+    index_select does) before anything runs; off, the kernels clamp it."""
+    from vdn_fp8 import fused_block as FB
+    torch.manual_seed(4)
+    lin = vdn_fp8.Fp8Linear(_copy_to(torch.nn.Linear(256, 256, dtype=torch.bfloat16), device))
+    qx, sx = vdn_fp8.quantize_rows(torch.randn(32, 256, dtype=torch.bfloat16, device=device))
+    gate = torch.rand(3, 256, device=device).to(torch.bfloat16)
+    bad = torch.tensor([0, 1, 2, 3] * 8, dtype=torch.int32, device=device)
+    x = torch.randn(32, 256, dtype=torch.bfloat16, device=device)
+    prev = vdn_fp8.set_index_checks(True)
+    try:
+        with pytest.raises(IndexError):
+            lin.forward_quantized(qx, sx, epilogue="gate", gate=gate, gate_index=bad)
+        with pytest.raises(IndexError):
+            FB.post(x, gate, bad, x)
+        with pytest.raises(IndexError):
+            FB.pre(x, None, 1e-6, gate, gate, bad)
+        ok = bad.clamp(0, 2)
+        lin.forward_quantized(qx, sx, epilogue="gate", gate=gate, gate_index=ok)
+    finally:
+        vdn_fp8.set_index_checks(prev)
+    clamped = lin.forward_quantized(qx, sx, epilogue="gate", gate=gate, gate_index=bad)
+    want = lin.forward_quantized(qx, sx, epilogue="gate", gate=gate, gate_index=bad.clamp(0, 2))
+    torch.cuda.synchronize()
+    assert torch.equal(clamped.view(torch.int16), want.view(torch.int16))

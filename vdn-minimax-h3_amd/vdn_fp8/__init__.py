@@ -10,7 +10,7 @@ block's pre-norm (`src.models.ops.fused_block`) with the quantization that follo
 from .fp8_linear import (FP8_DTYPE, MIN_WIDTH, SKIP_END_BLOCKS, _FP8_MAX, Fp8Linear,
                          convert_linear_to_fp8, per_tensor_gemm, quantize_activation,
                          quantize_rows, quantize_rows_reference, requantize_weight,
-                         swiglu_quantize, swiglu_quantize_activation)
+                         set_index_checks, swiglu_quantize, swiglu_quantize_activation)
 from .fused_block import fast_block_forward, fast_ff_forward, post, pre, pre_quantize
 from .lora import load_external_lora, merge_lora_and_convert, merge_lora_state
 from .softmax_attention import qk_prep
@@ -20,5 +20,5 @@ __all__ = [
     "per_tensor_gemm", "quantize_activation", "quantize_rows", "quantize_rows_reference",
     "requantize_weight", "swiglu_quantize", "swiglu_quantize_activation", "load_external_lora",
     "merge_lora_and_convert", "merge_lora_state", "pre_quantize", "qk_prep", "pre", "post",
-    "fast_ff_forward", "fast_block_forward",
+    "fast_ff_forward", "fast_block_forward", "set_index_checks",
 ]

@@ -23,6 +23,7 @@ the GEMM; `Fp8Linear(linear, lora=(A, B, scale))` quantizes W + scale * B @ A in
 kernel without writing the merged bf16 weight.
 """
 import ctypes
+import os
 
 import torch
 import torch.nn as nn
@@ -81,6 +82,32 @@ def gemm_workspace_bytes(M, N, K, device):
         _lib.check(_lib.load().vdn_fp8_gemm_workspace_size(M, N, K, ctypes.byref(out)), "gemm_workspace_size")
         _WS_BYTES[key] = out.value
     return _WS_BYTES[key]
+
+
+_CHECK_INDICES = os.environ.get("VDN_FP8_CHECK_INDICES", "") not in ("", "0")
+
+
+def set_index_checks(enabled):
+    """Table indices outside [0, rows) (the gate table of the GEMM's gate epilogue and of
+    `post`, the modulation tables of the pre-norm) are clamped into the table by the
+    kernels, where the reference's index_select raises. With checks enabled (or
+    VDN_FP8_CHECK_INDICES=1 in the environment) every such call first checks the range on
+    the device -- a reduction and a host synchronization per call -- and raises IndexError
+    as index_select does. Returns the previous setting."""
+    global _CHECK_INDICES
+    prev, _CHECK_INDICES = _CHECK_INDICES, bool(enabled)
+    return prev
+
+
+def check_index_range(indices, rows, what):
+    """Raises IndexError if `indices` (a tensor) holds a value outside [0, rows) and index
+    checks are enabled (set_index_checks); a no-op otherwise."""
+    if not _CHECK_INDICES or indices is None or indices.numel() == 0:
+        return
+    lo, hi = int(indices.min()), int(indices.max())
+    if lo < 0 or hi >= rows:
+        raise IndexError(f"{what}: index out of range in self (indices span [{lo}, {hi}], the table has "
+                         f"{rows} rows)")
 
 
 def quantize_rows(x):
@@ -245,9 +272,20 @@ class Fp8Linear(nn.Module):
     def __init__(self, linear: nn.Linear, *, lora=None):
         super().__init__()
         _rowwise_only()
-        q, s = requantize_weight(linear.weight.detach(), lora=lora)
-        self.register_buffer("weight_fp8", q)
-        self.register_buffer("weight_scale", s.reshape(1, -1).contiguous())
+        w = linear.weight.detach()
+        home = w.device
+        if not w.is_cuda:
+            # The reference's rowwise branch is eager torch on any device
+            # (fp8_linear.py:262-267); here the requantization is a HIP kernel, so a
+            # host-resident Linear is requantized on the current GPU and its buffers are
+            # returned to the Linear's device, as the reference's would live there.
+            if not torch.cuda.is_available():
+                raise ValueError("Fp8Linear needs a GPU: the fp8 requantizer is a HIP kernel "
+                                 f"(the Linear's weight is on {home})")
+            w = w.to(torch.device("cuda", torch.cuda.current_device()))
+        q, s = requantize_weight(w, lora=lora)
+        self.register_buffer("weight_fp8", q.to(home))
+        self.register_buffer("weight_scale", s.reshape(1, -1).contiguous().to(home))
         self.register_parameter("bias", linear.bias)
 
     @property
@@ -308,6 +346,7 @@ class Fp8Linear(nn.Module):
                 gi = _aligned16(gate_index.to(device=dev, dtype=torch.int32).contiguous())
                 if gi.numel() != M:
                     raise ValueError("gate_index must hold one table row per token")
+                check_index_range(gi, grows, "gate_index")
             if residual is not None:
                 res = residual.detach()
                 if res.device != dev:

@@ -26,7 +26,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .fp8_linear import (FP8_DTYPE, Fp8Linear, _aligned16, _ptr, _rows, _stream,
+from .fp8_linear import (FP8_DTYPE, Fp8Linear, _aligned16, _ptr, _rows, _stream, check_index_range,
                          swiglu_quantize_activation)
 
 
@@ -87,6 +87,7 @@ def _pre_args(x, weight, scale, shift, indices):
             idx = indices.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
             if idx.numel() != M:
                 raise ValueError("indices must hold one table row per token")
+            check_index_range(idx, rows, "pre: indices")
     elif indices is not None:
         raise ValueError("indices need a scale/shift table")
     return w, sc, sh, ld, idx, rows
@@ -153,6 +154,7 @@ def post(residual, gate, indices, branch_out):
         idx = indices.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
         if idx.numel() != M:
             raise ValueError("indices must hold one table row per token")
+        check_index_range(idx, g.shape[0], "post: indices")
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     lib = _lib.load()
     _lib.check(lib.vdn_fp8_gated_residual(_ptr(r), r.stride(0), _ptr(g), N, _ptr(idx), g.shape[0], _ptr(b),
