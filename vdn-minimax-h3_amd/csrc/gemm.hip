@@ -104,8 +104,10 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& p, int nk, int v, int&
         const int r = __builtin_amdgcn_readfirstlane(unit / p.splits);
         const int sl = unit - r * p.splits;
         tile = p.t_main + r;
-        kb0 = __builtin_amdgcn_readfirstlane(sl * nk / p.splits);
-        cnt = __builtin_amdgcn_readfirstlane((sl + 1) * nk / p.splits) - kb0;
+        // (slice boundaries on even blocks: the K loop takes blocks two at a time)
+        const int h = nk >> 1;
+        kb0 = 2 * __builtin_amdgcn_readfirstlane(sl * h / p.splits);
+        cnt = 2 * __builtin_amdgcn_readfirstlane((sl + 1) * h / p.splits) - kb0;
     }
 }
 
@@ -251,6 +253,14 @@ __device__ __forceinline__ void wave_sync_vm()
 // ---------------------------------------------------------------------------
 // main kernel: K % 128 == 0, persistent
 // ---------------------------------------------------------------------------
+// Row r, 16-byte chunk c (0..7) of a 128-byte-row LDS tile sits at chunk c ^ s(r),
+// s(r) = bits 1, 0, 2 of r. A 16 x 128-byte fragment read (lane L: row L % 16, chunk
+// 2 (L / 16), then the next chunk) runs without bank conflicts under this swizzle --
+// measured over every XOR swizzle of the row's low four bits: 1342 of the 4096 run at
+// the full rate, the XOR with bits 1..3 of the row (conflict-free for the 32-row reads
+// of the 32 x 32 x 64 instruction) at half of it.
+__device__ __forceinline__ int row_swizzle(int row) { return ((row >> 1) & 1) | ((row & 1) << 1) | (row & 4); }
+
 namespace mainloop {
 constexpr int BK = 128;                     // K bytes per block (one LDS stage)
 constexpr int kStage = (BM + BN) * BK;      // 64 KiB: X tile, then W tile
@@ -266,9 +276,7 @@ constexpr int kEpiStores = 32;              // 16-byte stores per wave per tile 
 constexpr int kStoreNT = 2;                 // cache policy of the output stores: non-temporal (the
                                             // output streams; keeps L2 for the operand panels)
 
-// Row r, 16-byte chunk c (0..7) of a tile sits at chunk c ^ ((r >> 1) & 7) of
-// its 128-byte LDS row.
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ row_swizzle(row)) << 4); }
 }  // namespace mainloop
 
 __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
@@ -281,9 +289,10 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 }
 
 // Epilogue of the tile at (m0, n0) with its vectors in scalar buffer sb of smem
-// acc[t][u][r] is n = wn*128 + 32 t + 8 (r/4) + 4 (lane/32) + r%4, m = wm*128 +
-// 32 u + lane%32 (tile-relative). Per u and per 64-column half th the wave
-// finishes its 32 x 64 slab in that layout (4 consecutive n per lane),
+// acc[i][j][e] is n = wn*128 + 16 i + 4 (lane/16) + e, m = wm*128 + 16 j +
+// lane%16 (tile-relative). Per 32-row band u and per 64-column half th the wave
+// finishes its 32 x 64 slab (accumulators i = 4 th .. 4 th + 3, j = 2 u, 2 u + 1)
+// in that layout (4 consecutive n per lane),
 // writes it to its staging (32 rows of 128 bytes, padded to 144), reads it
 // back by rows and stores 16-byte pieces of whole 128-byte row segments: lane
 // L covers row 8 i + L/8, channels 8 (L%8) .. +7. The gate and residual
@@ -293,7 +302,7 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // reduction.
 template <int EPI, bool FAST>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* scal, uint8_t* stg,
-                                              f32x16_t (&acc)[4][4], int64_t m0, int64_t n0, int wave)
+                                              f32x4_t (&acc)[8][8], int64_t m0, int64_t n0, int wave)
 {
     using namespace mainloop;
     const int wn = wave & 1, wm = wave >> 1;
@@ -305,7 +314,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
     uint32_t zero;
     asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
     const int el = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
-    const int frow = el & 31, fh = el >> 5, cc = el & 7, rl = el >> 3;
+    const int fr = el & 15, fg = el >> 4, cc = el & 7, rl = el >> 3;
     const float* s_sw = reinterpret_cast<const float*>(scal);
     const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
     const uint16_t* s_bias = reinterpret_cast<const uint16_t*>(scal + 2048);
@@ -322,49 +331,46 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
     // slab's values overwrite it (a wave's LDS operations run in order), so its
     // computation hides that read's latency.
     const bool has_bias = p.bias != nullptr;
-    float hsw[2][4][4], hb[2][4][4], hg[2][4][4];
+    float hsw[4][4], hb[4][4], hg[4][4];
     auto hoist = [&](int th) {
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int nl = wn * 128 + 32 * (2 * th + t2) + 8 * q + 4 * fh;
-                const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
-                hsw[t2][q][0] = sw.x; hsw[t2][q][1] = sw.y; hsw[t2][q][2] = sw.z; hsw[t2][q][3] = sw.w;
-                if (has_bias) {
-                    const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
-                    hb[t2][q][0] = bf16_lo(b.x); hb[t2][q][1] = bf16_hi(b.x);
-                    hb[t2][q][2] = bf16_lo(b.y); hb[t2][q][3] = bf16_hi(b.y);
-                }
-                if (EPI == VDN_FP8_EPI_GATE && FAST) {
-                    const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
-                    hg[t2][q][0] = bf16_lo(gv.x); hg[t2][q][1] = bf16_hi(gv.x);
-                    hg[t2][q][2] = bf16_lo(gv.y); hg[t2][q][3] = bf16_hi(gv.y);
-                }
+        for (int ii = 0; ii < 4; ++ii) {
+            const int nl = wn * 128 + 64 * th + 16 * ii + 4 * fg;
+            const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
+            hsw[ii][0] = sw.x; hsw[ii][1] = sw.y; hsw[ii][2] = sw.z; hsw[ii][3] = sw.w;
+            if (has_bias) {
+                const uint2 b = *reinterpret_cast<const uint2*>(s_bias + nl);
+                hb[ii][0] = bf16_lo(b.x); hb[ii][1] = bf16_hi(b.x);
+                hb[ii][2] = bf16_lo(b.y); hb[ii][3] = bf16_hi(b.y);
             }
+            if (EPI == VDN_FP8_EPI_GATE && FAST) {
+                const uint2 gv = *reinterpret_cast<const uint2*>(s_gate + nl);
+                hg[ii][0] = bf16_lo(gv.x); hg[ii][1] = bf16_hi(gv.x);
+                hg[ii][2] = bf16_lo(gv.y); hg[ii][3] = bf16_hi(gv.y);
+            }
+        }
     };
     // bf16 GEMM output, then the bf16 bias add: each rounding done two values per
     // conversion, the second one's pairs being the stored words (opaque, so the
     // compiler keeps the pairs); one uniform branch per slab
     auto compute = [&](int th, int u, auto with_bias) {
-        const float sxm = s_sx[wm * 128 + 32 * u + frow];
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
+        for (int jj = 0; jj < 2; ++jj) {
+            const float sxm = s_sx[wm * 128 + 32 * u + 16 * jj + fr];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int t = 2 * th + t2;
-                const float* sw = hsw[t2][q];
+            for (int ii = 0; ii < 4; ++ii) {
+                const float* sw = hsw[ii];
                 // A rounding to bf16 that the bias add or GELU reads is one conversion per
                 // value (round_bf16_hi: no unpacking); the last one converts the stored
                 // pairs. The gate kernels keep the packed pairs and unpack them (one value
                 // per conversion there made the compiler spill).
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[t][u][4 * q + e] * (sxm * sw[e]);
+                for (int e = 0; e < 4; ++e) v[e] = acc[4 * th + ii][2 * u + jj][e] * (sxm * sw[e]);
                 uint32_t r01, r23;
                 if (EPI != VDN_FP8_EPI_GATE) {
                     if (decltype(with_bias)::value) {
-                        const float* bb = hb[t2][q];
+                        const float* bb = hb[ii];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = round_bf16_hi(v[e]) + bb[e];
                     }
@@ -380,22 +386,26 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
                     r23 = pack_bf16x2(v[2], v[3]);
                     asm volatile("" : "+v"(r01), "+v"(r23));
                     if (decltype(with_bias)::value) {
-                        const float* bb = hb[t2][q];
+                        const float* bb = hb[ii];
                         r01 = pack_bf16x2(bf16_lo(r01) + bb[0], bf16_hi(r01) + bb[1]);
                         r23 = pack_bf16x2(bf16_lo(r23) + bb[2], bf16_hi(r23) + bb[3]);
                         asm volatile("" : "+v"(r01), "+v"(r23));
                     }
                     if (FAST) {   // broadcast gate row, no residual
-                        const float* gg = hg[t2][q];
+                        const float* gg = hg[ii];
                         r01 = pack_bf16x2(bf16_lo(r01) * gg[0], bf16_hi(r01) * gg[1]);
                         r23 = pack_bf16x2(bf16_lo(r23) * gg[2], bf16_hi(r23) * gg[3]);
                     }
                 }
-                *reinterpret_cast<uint2*>(stg + frow * kStgRow + ((4 * t2 + q) << 4) + (fh << 3)) = make_uint2(r01, r23);
+                *reinterpret_cast<uint2*>(stg + (16 * jj + fr) * kStgRow + 32 * ii + 8 * fg) = make_uint2(r01, r23);
             }
+        }
         // these accumulators start the next tile from zero
-        acc[2 * th][u] = f32x16_t{};
-        acc[2 * th + 1][u] = f32x16_t{};
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            acc[4 * th + ii][2 * u] = f32x4_t{};
+            acc[4 * th + ii][2 * u + 1] = f32x4_t{};
+        }
     };
     // fast path: the slab's rows 8 i + L/8 from the staging, then their stores (byte
     // offset of the row, or out of range past N)
@@ -523,15 +533,25 @@ void k_gemm_fp8(GemmArgs p)
 
     // Copies: this wave fills rows 64 wave .. 64 wave + 63 of each tile, 8 rows
     // (1 KiB) per copy. Lane L lands at row +L/8, physical chunk L%8, so it
-    // fetches logical chunk (L%8) ^ ((row >> 1) & 7), row = 64 wave + 8 i + L/8.
+    // fetches logical chunk (L%8) ^ row_swizzle(row), row = 64 wave + 8 i + L/8.
+    // (recomputed per tile from an opaque lane index, with every other lane-dependent
+    // value of the K loop, so that none is held in registers across the epilogue)
     uint32_t xoff[kCopies], woff[kCopies];
+    auto opaque_lane = [&]() -> int {
+        uint32_t zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        return (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
+    };
+    auto copy_offsets = [&](int l) {
 #pragma unroll
-    for (int i = 0; i < kCopies; ++i) {
-        const int r = 64 * wave + 8 * i + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        xoff[i] = (uint32_t)(r * p.ldx) + c * 16;
-        woff[i] = (uint32_t)(r * p.ldw) + c * 16;
-    }
+        for (int i = 0; i < kCopies; ++i) {
+            const int r = 64 * wave + 8 * i + (l >> 3);
+            const int c = (l & 7) ^ row_swizzle(r);
+            xoff[i] = (uint32_t)(r * p.ldx) + c * 16;
+            woff[i] = (uint32_t)(r * p.ldw) + c * 16;
+        }
+    };
+    copy_offsets(lane);
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)smem;
 
     // Producer: the next block to copy is block pj of item pv (pnk blocks from block
@@ -607,28 +627,8 @@ void k_gemm_fp8(GemmArgs p)
         copy16_to_lds(r, lds_base + kScal + buf * 4096 + wave * 1024, l * 16, 0);
     };
 
-    // Fragments of half h (k bytes 64 h .. 64 h + 63) of the block in stage st:
-    // lane reads row (base + lane % 32), k bytes 64 h + 32 (lane / 32) .. +31, as
-    // two 16-byte chunks. Fragment f < 4 is W rows wn*128 + 32 f.., f >= 4 is X
-    // rows wm*128 + 32 (f-4)..
-    const int frow = lane & 31, fh = lane >> 5;
-    auto read_frag = [&](int st, int h, int f) -> i32x8_t {
-        const uint8_t* s = smem + st * kStage + (f < 4 ? BM * BK : 0);
-        const int row = (f < 4 ? wn * 128 + 32 * f : wm * 128 + 32 * (f - 4)) + frow;
-        const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh));
-        const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 4 * h + 2 * fh + 1));
-        return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    };
-    f32x16_t acc[4][4];
-    // MFMA q (0..15) of a half-step: acc[t][u] += W frag t x X frag u, t = q % 4, u = q / 4.
-    auto mfma = [&](const i32x8_t* wf, const i32x8_t* xf, int q) {
-        const int t = q & 3, u = q >> 2;
-        acc[t][u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t], xf[u], acc[t][u], 0, 0, 0, 0, 0, 0);
-    };
-    auto read_into = [&](int st, int h, int f, i32x8_t* wf, i32x8_t* xf) {
-        if (f < 4) wf[f] = read_frag(st, h, f);
-        else xf[f - 4] = read_frag(st, h, f);
-    };
+    // acc[i][j] += W fragment i x X fragment j: 16 (n) x 16 (m) outputs over the whole block
+    f32x4_t acc[8][8];
     auto fence = [&]() { __builtin_amdgcn_sched_barrier(0); };
 
     auto epilogue = [&](int64_t m0, int64_t n0, int sb) {
@@ -646,16 +646,19 @@ void k_gemm_fp8(GemmArgs p)
     for (int c = 0; c < kBlockCopies; ++c) copy(1, (c + kCopies) % kBlockCopies);
     advance();
 
-    i32x8_t w0[4], x0[4], w1[4], x1[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][u] = f32x16_t{};   // the epilogue re-zeroes them per tile
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{};   // the epilogue re-zeroes them per tile
     int g = 0;    // stream index of the block being computed
     int k = 0;    // tiles done by this workgroup
+
     for (int v = v_begin + blockIdx.x; v < n_items; v += stride, ++k) {
         int tile, kb0, cnt, unit, tm, tn;
         gemm_item<PARTIAL>(p, nk, v, tile, kb0, cnt, unit);
+        // (opaque: conditions on it are then evaluated per block, not hoisted out of
+        // the tile loop into registers held across the epilogue)
+        asm volatile("" : "+s"(cnt));
         tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
         // Block g has landed once only block g+1's copies -- and, after the first
@@ -663,71 +666,100 @@ void k_gemm_fp8(GemmArgs p)
         if (k == 0) wave_sync<kBlockCopies>();
         else wave_sync<kBlockCopies + kE>();
         scal_copy(v + stride, (k + 1) & 1);   // every wave is past the epilogue that used that buffer
-#pragma unroll
-        for (int f = 0; f < 8; ++f) read_into(g & 1, 0, f, w0, x0);
-
-        for (int j = 0; j < cnt; ++j, ++g) {
+        const int el = opaque_lane();
+        copy_offsets(el);
+        // Fragments of the block in stage st: 16 rows x 128 K bytes; lane L reads row
+        // (base + L % 16), k bytes 32 (L / 16) .. +31, as two 16-byte chunks. W fragment
+        // i is W rows wn*128 + 16 i .., X fragment j is X rows wm*128 + 16 j ..
+        const int fr = el & 15, fg = el >> 4;
+        auto read_frag = [&](const uint8_t* s, int row) -> i32x8_t {
+            const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg));
+            const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg + 1));
+            return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        };
+        auto read_w = [&](int st, int i) { return read_frag(smem + st * kStage + BM * BK, wn * 128 + 16 * i + fr); };
+        auto read_x = [&](int st, int j) { return read_frag(smem + st * kStage, wm * 128 + 16 * j + fr); };
+        // W fragments of the block being computed and of the next one (read into the
+        // other set while this block's MFMAs run); X fragments two at a time. (Declared
+        // per tile: nothing of them lives across the epilogue.)
+        i32x8_t wa[8], wb[8], xf[2];
+        // Block g (j-th of the tile's cnt blocks, stage st = g % 2): 8 groups of 8 MFMAs,
+        // group jx multiplying X fragment jx by the 8 W fragments.
+        //   start (P0): W copies of block g+1 have landed in every wave, and every wave
+        //     is done reading block g's W fragments (read during block g-1, or at the
+        //     tile's start); group 1 then issues the W copies of block g+2 into stage st.
+        //   group jx reads X fragment jx+1 (group 7: block g+1's X fragment 0) and W
+        //     fragment jx of block g+1.
+        //   group 7 (P7): X copies of block g+1 have landed, every wave is done with block
+        //     g's X fragments (the last read in group 6); group 7 issues the X copies of
+        //     block g+2 into stage st.
+        // Copies newer than the awaited ones at P0 and P7: 8, plus in a tile's first block
+        // the previous epilogue's stores and the vector copy. The tile's last block reads
+        // the next one's fragments too (those of the next tile's first block, which the
+        // next tile reads again): one code path, so the compiler's LDS waits count only
+        // what each MFMA needs.
+        // odd: which W set is current (wa in even blocks).
+        auto kblock = [&](auto odd, int j) {
+            i32x8_t (&wc)[8] = decltype(odd)::value ? wb : wa;
+            i32x8_t (&wx)[8] = decltype(odd)::value ? wa : wb;
             const int st = g & 1;
-            const bool more = j + 1 < cnt;
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                mfma(w0, x0, q);
-                fence();
-                if (q < 4) {
-                    read_into(st, 1, 2 * q, w1, x1);
-                    read_into(st, 1, 2 * q + 1, w1, x1);
+            auto sync = [&]() {
+                if (j > 0) wave_sync<kCopies>();
+                else if (k > 0) wave_sync<kCopies + 1 + kE>();
+                else wave_sync<kCopies + 1>();
+            };
+            sync();
+    #pragma unroll
+            for (int jx = 0; jx < 8; ++jx) {
+                if (jx == 7) sync();
+    #pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    acc[i][jx] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[i], xf[jx & 1], acc[i][jx],
+                                                                                   0, 0, 0, 0, 0, 0);
+                    fence();
+                    if (i == 0) xf[(jx + 1) & 1] = jx < 7 ? read_x(st, jx + 1) : read_x(st ^ 1, 0);
+                    if (i == 1) wx[jx] = read_w(st ^ 1, jx);
+                    if (jx == 1) copy(st, kCopies + i);   // W copies of block g+2
+                    if (jx == 7) copy(st, i);             // X copies of block g+2
+                    if (jx == 7 && i == 7) advance();
+                    fence();
                 }
-                if (q == 7) wave_sync<kNoVmWait>();
-                if (q >= 8) copy(st, q);             // W copies of block g+2
-                fence();
             }
+            ++g;
+        };
+
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                mfma(w1, x1, q);
-                fence();
-                if (q < 8) copy(st, q);              // X copies of block g+2
-                if (q == 7) {
-                    advance();
-                    // W of block g+1 has landed: newer are its X copies, block g+2's
-                    // copies and, in a tile's first block, the previous epilogue's
-                    // stores and the vector copy.
-                    if (j == 0 && k > 0) wave_sync<kCopies + kBlockCopies + 1 + kE>();
-                    else if (j == 0) wave_sync<kCopies + kBlockCopies + 1>();
-                    else wave_sync<kCopies + kBlockCopies>();
-                }
-                if (q == 11) {
-                    // X of block g+1 has landed
-                    if (j == 0 && k > 0) wave_sync_vm<kBlockCopies + 1 + kE>();
-                    else if (j == 0) wave_sync_vm<kBlockCopies + 1>();
-                    else wave_sync_vm<kBlockCopies>();
-                }
-                if (q >= 8 && more) read_into(st ^ 1, 0, q - 8, w0, x0);   // W fragments, then X
-                fence();
-            }
+        for (int i = 0; i < 8; ++i) wa[i] = read_w(g & 1, i);
+        xf[0] = read_x(g & 1, 0);
+        // blocks 0, 1, .. cnt-1 (cnt even) alternate W sets (even: wa current)
+        for (int j = 0; j < cnt; j += 2) {
+            kblock(std::false_type{}, j);
+            kblock(std::true_type{}, j + 1);
         }
         if constexpr (!PARTIAL) {
             epilogue(m0, n0, k & 1);
         } else {
-            // A split unit stores its partial sums in accumulator layout: float4 r4 of accumulator (t, u)
-            // of lane L at ((wave * 16 + 4 t + u) * 4 + r4) * 256 + 4 L of the unit's
-            // 65536 floats, one whole KiB per wave store.
-            // (a buffer descriptor over the wave's 64 KiB, one accumulator's four stores at a
-            // time: the 256 accumulators are not all moved to VGPRs at once)
+            // (the launch has one workgroup per unit, so this is the workgroup's only item and
+            // the accumulators are not re-zeroed)
+            // A split unit stores its partial sums in accumulator layout: accumulator (i, j) of
+            // lane L at (wave * 64 + 8 i + j) * 256 + 4 L of the unit's 65536 floats, one whole
+            // KiB per wave store (a buffer descriptor over the wave's 64 KiB, four stores at a
+            // time: the 256 accumulators are not all moved to VGPRs at once).
             const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)(p.ws + ((int64_t)unit * 4 + wave) * 16384), 0, 65536, kRsrcWord3);
             uint32_t zero;
             asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
             const uint32_t l16 = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero) * 16;
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+            for (int i = 0; i < 8; ++i)
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int j4 = 0; j4 < 2; ++j4) {
 #pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4)
-                        __builtin_amdgcn_raw_buffer_store_b128(
-                            __builtin_bit_cast(i32x4_t, f32x4_t{acc[t][u][4 * r4], acc[t][u][4 * r4 + 1],
-                                                                acc[t][u][4 * r4 + 2], acc[t][u][4 * r4 + 3]}),
-                            wsr, l16, ((4 * t + u) * 4 + r4) * 1024, 0);
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const int j = 4 * j4 + jj;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, acc[i][j]), wsr, l16,
+                                                               (8 * i + j) * 1024, 0);
+                    }
                     settle_stores();
                 }
         }
@@ -801,15 +833,9 @@ void k_gemm_splitk_reduce(GemmArgs p)
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    f32x16_t acc[4][4];
+    f32x4_t acc[8][8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[t][u][4 * r4 + e] = a[(4 * t + u) * 4 + r4][e];
+    for (int i = 0; i < 64; ++i) acc[i >> 3][i & 7] = a[i];
     __syncthreads();
     tile_epilogue<EPI, FAST>(p, scal, stg, acc, m0, n0, quad);
 }
@@ -821,7 +847,7 @@ namespace tailloop {
 constexpr int BK = 128;
 constexpr int kStage = (BM + BN) * BK;
 constexpr int kChunks = BM * BK / 16 / kThreads;  // 8
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * BK + ((chunk ^ row_swizzle(row)) << 4); }
 }  // namespace tailloop
 
 template <int EPI>
@@ -948,7 +974,7 @@ struct SplitPlan {
 __host__ inline SplitPlan plan_split(int64_t T, int grid, int64_t K)
 {
     SplitPlan sp{(int)T, 0, 0};
-    if (K < kSplitMinK || K % mainloop::BK || grid <= 0) return sp;
+    if (K < kSplitMinK || K % (2 * mainloop::BK) || grid <= 0) return sp;
     const int64_t R = T % grid;
     if (R == 0 || R > grid / 2) return sp;
     const int64_t S = std::min<int64_t>(grid / R, K / mainloop::BK / kSplitMinBlocks);
@@ -1014,7 +1040,7 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
                (const uint16_t*)residual, ldres, (uint16_t*)out, ldo, (int)tiles_m, (int)tiles_n,
                kPhaseMod, kPhaseStep, kGroupM, (int)T, 0, 0, nullptr};
     tile_order(N, K, p.k_phase_mod, p.group_m);
-    const bool main = (K % mainloop::BK) == 0;
+    const bool main = (K % (2 * mainloop::BK)) == 0;
     int64_t blocks = T;
     if (main) {
         const int cus = device_cus();
