@@ -10,20 +10,24 @@
 // Both operands are K-contiguous (xq [M, K], wq [N, K]), the "TN" layout of
 // torch._scaled_mm(x_fp8, weight_fp8.t()) in the reference (fp8_linear.py:272).
 //
-// Main kernel (K % 128 == 0). A workgroup of 4 wavefronts computes a 256 (m) x
-// 256 (n) output tile; each wave owns a 128 x 128 quadrant as 4 x 4
-// v_mfma_f32_32x32x64_f8f6f4 tiles (256 fp32 accumulators per lane, in AGPRs).
+// Main kernel (K % 256 == 0). A workgroup of 4 wavefronts computes a 256 (m) x
+// 256 (n) output tile; each wave owns a 128 x 128 quadrant as 8 x 8
+// v_mfma_f32_16x16x128_f8f6f4 tiles (256 fp32 accumulators per lane, in AGPRs).
 // K advances in 128-byte blocks through two LDS stages (X and W tiles of 256
 // rows x 128 bytes: 64 KiB a stage). Global -> LDS copies bypass VGPRs
 // (buffer_load_dwordx4 ... lds) and move whole 128-byte rows -- half-line
-// copies stream at two thirds of the rate on this part. Each block is
-// consumed as two half-steps of 16 MFMAs; the next half-step's operand
-// fragments are read from LDS into a second VGPR set while the current
-// half-step's MFMAs run, and the copies of block j+2 are issued as soon as
-// every wave is done with block j (one barrier per block).
-// LDS rows are 128 bytes; the 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7),
-// so the 16 rows a 16-lane group reads hit 16 distinct 16-byte bank groups of
-// gfx950's 64 banks (no conflicts for ds_read_b128).
+// copies stream at two thirds of the rate on this part. A block is 64 MFMAs,
+// each over the whole 128 K bytes: 8 groups, group j multiplying X fragment j by
+// the wave's 8 W fragments. The W fragments sit in registers for the block, the
+// next block's are read into a second set while this one's MFMAs run (so blocks
+// come in pairs: K a multiple of 256), and the X fragments stream three groups
+// ahead of their MFMAs. Two barriers per block free the W and X halves of a stage
+// for the copies of block j+2. On random operand codes the 16 x 16 x 128
+// instruction reaches 0.88 of the nominal peak in a bare loop where the
+// 32 x 32 x 64 one reaches 0.75 (the part is power-limited and the smaller
+// instruction draws less per FLOP).
+// LDS rows are 128 bytes; the 16-byte chunk c of row r sits at c ^ s(r) (see
+// row_swizzle: conflict-free for the 16-row fragment reads).
 //
 // MFMA orientation: the instruction's A operand is the W tile (its rows are
 // output channels n) and its B operand the X tile (columns are tokens m), so
@@ -680,20 +684,21 @@ void k_gemm_fp8(GemmArgs p)
         auto read_w = [&](int st, int i) { return read_frag(smem + st * kStage + BM * BK, wn * 128 + 16 * i + fr); };
         auto read_x = [&](int st, int j) { return read_frag(smem + st * kStage, wm * 128 + 16 * j + fr); };
         // W fragments of the block being computed and of the next one (read into the
-        // other set while this block's MFMAs run); X fragments two at a time. (Declared
-        // per tile: nothing of them lives across the epilogue.)
-        i32x8_t wa[8], wb[8], xf[2];
+        // other set while this block's MFMAs run); X fragments four at a time, in rotation.
+        // (Declared per tile: nothing of them lives across the epilogue.)
+        i32x8_t wa[8], wb[8], xf[4];
         // Block g (j-th of the tile's cnt blocks, stage st = g % 2): 8 groups of 8 MFMAs,
         // group jx multiplying X fragment jx by the 8 W fragments.
         //   start (P0): W copies of block g+1 have landed in every wave, and every wave
         //     is done reading block g's W fragments (read during block g-1, or at the
         //     tile's start); group 1 then issues the W copies of block g+2 into stage st.
-        //   group jx reads X fragment jx+1 (group 7: block g+1's X fragment 0) and W
-        //     fragment jx of block g+1.
-        //   group 7 (P7): X copies of block g+1 have landed, every wave is done with block
-        //     g's X fragments (the last read in group 6); group 7 issues the X copies of
-        //     block g+2 into stage st.
-        // Copies newer than the awaited ones at P0 and P7: 8, plus in a tile's first block
+        //   group jx reads X fragment jx+3 (groups 5-7: block g+1's X fragments 0-2), three
+        //     groups ahead of its MFMAs (one group ahead left them waiting on the read), and
+        //     W fragment jx of block g+1.
+        //   group 5 (P5): X copies of block g+1 have landed, every wave is done with block
+        //     g's X fragments (the last read in group 4); groups 5 and 6 issue the X copies
+        //     of block g+2 into stage st.
+        // Copies newer than the awaited ones at P0 and P5: 8, plus in a tile's first block
         // the previous epilogue's stores and the vector copy. The tile's last block reads
         // the next one's fragments too (those of the next tile's first block, which the
         // next tile reads again): one code path, so the compiler's LDS waits count only
@@ -711,17 +716,17 @@ void k_gemm_fp8(GemmArgs p)
             sync();
     #pragma unroll
             for (int jx = 0; jx < 8; ++jx) {
-                if (jx == 7) sync();
+                if (jx == 5) sync();
     #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    acc[i][jx] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[i], xf[jx & 1], acc[i][jx],
+                    acc[i][jx] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[i], xf[jx & 3], acc[i][jx],
                                                                                    0, 0, 0, 0, 0, 0);
                     fence();
-                    if (i == 0) xf[(jx + 1) & 1] = jx < 7 ? read_x(st, jx + 1) : read_x(st ^ 1, 0);
+                    if (i == 0) xf[(jx + 3) & 3] = jx < 5 ? read_x(st, jx + 3) : read_x(st ^ 1, jx - 5);
                     if (i == 1) wx[jx] = read_w(st ^ 1, jx);
                     if (jx == 1) copy(st, kCopies + i);   // W copies of block g+2
-                    if (jx == 7) copy(st, i);             // X copies of block g+2
-                    if (jx == 7 && i == 7) advance();
+                    if ((jx == 5 || jx == 6) && (i & 1)) copy(st, 4 * (jx - 5) + (i >> 1));   // X copies of block g+2
+                    if (jx == 6 && i == 7) advance();
                     fence();
                 }
             }
@@ -731,6 +736,8 @@ void k_gemm_fp8(GemmArgs p)
 #pragma unroll
         for (int i = 0; i < 8; ++i) wa[i] = read_w(g & 1, i);
         xf[0] = read_x(g & 1, 0);
+        xf[1] = read_x(g & 1, 1);
+        xf[2] = read_x(g & 1, 2);
         // blocks 0, 1, .. cnt-1 (cnt even) alternate W sets (even: wa current)
         for (int j = 0; j < cnt; j += 2) {
             kblock(std::false_type{}, j);
