@@ -170,18 +170,20 @@ def _probe_lib():
 
 
 def _mfma_ceiling(lib, xq, wq, blocks, grid, reps):
-    """The bare fp8 MFMA loop (the GEMM's grid, K-loop instruction mix and LDS fragment
-    reads, no copies, no epilogue) on the GEMM's own codes, on uniform codes, and with the
-    fragments held in registers: ms, TFLOP/s, fraction of the dense peak, and the clock and
-    power amd-smi reads while it runs back to back."""
+    """The bare fp8 MFMA loop (the GEMM's grid, instruction and LDS fragment reads, no
+    copies, no epilogue) on the GEMM's own codes, on uniform codes, and with the fragments
+    held in registers, and the 32 x 32 x 64 instruction on the same codes: ms, TFLOP/s,
+    fraction of the dense peak, and the clock and power amd-smi reads while it runs back to
+    back."""
     import ctypes
     import torch
     out = torch.empty(grid * 256, dtype=torch.float32, device=xq.device)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     flop = grid * 4 * blocks * 32 * (2 * 32 * 32 * 64)
     tiles = min(xq.shape[0], wq.shape[0]) // 256
-    res = {}
-    for name, mode in (("random_codes", 0), ("uniform_codes", 1), ("random_codes_registers_only", 2)):
+    res = {"instruction": "v_mfma_f32_16x16x128_f8f6f4 (the GEMM's)"}
+    for name, mode in (("random_codes", 3), ("uniform_codes", 4), ("random_codes_registers_only", 5),
+                       ("v_mfma_f32_32x32x64_f8f6f4_random_codes", 0)):
         def call():
             rc = lib.vdn_mfma_probe(mode, ctypes.c_void_p(xq.data_ptr()), ctypes.c_void_p(wq.data_ptr()),
                                     xq.stride(0), tiles, blocks, grid, ctypes.c_void_p(out.data_ptr()), stream)

@@ -723,8 +723,8 @@ void k_gemm_fp8(GemmArgs p)
                                                                                    0, 0, 0, 0, 0, 0);
                     fence();
                     if (i == 0) xf[(jx + 3) & 3] = jx < 5 ? read_x(st, jx + 3) : read_x(st ^ 1, jx - 5);
-                    if (i == 1) wx[jx] = read_w(st ^ 1, jx);
-                    if (jx == 1) copy(st, kCopies + i);   // W copies of block g+2
+                    if (i == 4) wx[jx] = read_w(st ^ 1, jx);
+                    if (jx >= 1 && jx <= 4 && (i == 2 || i == 6)) copy(st, kCopies + 2 * (jx - 1) + (i == 6));   // W copies of block g+2
                     if ((jx == 5 || jx == 6) && (i & 1)) copy(st, 4 * (jx - 5) + (i >> 1));   // X copies of block g+2
                     if (jx == 6 && i == 7) advance();
                     fence();
