@@ -2,9 +2,10 @@
 output is then the accumulator itself, rounded once), and set against the reference's own
 call on this part (torch._scaled_mm with fast accumulation, hipBLASLt).
 
-Known answers: inside one v_mfma_f32_32x32x64_f8f6f4 (64 products of one K step) the
-products are aligned to the largest of them before they are summed, and bits below that
-alignment are dropped. A cancelling pair of large products next to many small ones loses
+Known answers: inside one fp8 MFMA instruction (v_mfma_f32_16x16x128_f8f6f4 here: 128
+products of one K step; the 32 x 32 x 64 form behaves the same on its 64) the products are
+aligned to the largest of them before they are summed, and bits below that alignment are
+dropped. A cancelling pair of large products next to many small ones loses
 part of the small ones' sum (448^2 pairs with 62 products of 2^-9: 0.109 instead of 0.121),
 while the same small products alone sum exactly, as do exact small integers. hipBLASLt
 gives the same results on the same codes: it is the instruction's arithmetic, not this

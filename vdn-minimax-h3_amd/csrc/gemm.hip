@@ -497,15 +497,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
 
 // One workgroup per CU walks tiles blockIdx.x, + gridDim.x, ... The copies form
 // one stream of 128-byte K blocks across those tiles, so the next tile's first
-// two blocks are in flight while this tile's epilogue runs. Per block g (stage
-// g % 2), two half-steps of 16 MFMAs:
-//   half 0: MFMAs 0-3 read the half-1 fragments of g; barrier A after MFMA 7
-//     (stage g % 2 is then free); MFMAs 8-15 issue the W copies of block g+2.
-//   half 1: MFMAs 0-7 issue the X copies of block g+2; after MFMA 7 this
-//     wave's W copies of block g+1 have landed (newer ones may be pending) and
-//     all waves meet (barrier B); MFMAs 8-11 read the W fragments of g+1's
-//     first half; after MFMA 11 the same for its X copies (barrier C); MFMAs
-//     12-15 read its X fragments. W goes first because it is read first.
+// two blocks are in flight while this tile's epilogue runs. The block schedule
+// (8 groups of 8 MFMAs, two barriers) is described at the K loop below.
 // A tile's vectors (w_scale, x_scale, bias, gate rows) are copied into one of
 // two scalar buffers at the start of the tile before, one copy per wave. The
 // epilogue stages through LDS of its own.

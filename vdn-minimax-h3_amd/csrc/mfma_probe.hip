@@ -3,12 +3,12 @@
 // stream, no epilogue, no output -- as a ceiling to set the GEMM's rate against.
 // Not part of the product's C ABI (libvdnprobe.so, loaded by bench.py only).
 //
-// Same grid and instruction mix as the GEMM's K loop: one workgroup of four
-// waves per CU (one wave per SIMD), each wave 4 x 4 v_mfma_f32_32x32x64_f8f6f4
-// accumulators (a 128 x 128 quadrant), a block of 128 K bytes consumed as two
-// half-steps of 16 MFMAs whose operand fragments are read from LDS (16-byte
-// reads, the GEMM's swizzled 128-byte rows) while the previous half-step's
-// MFMAs run. The LDS stage is filled once from the caller's e4m3 codes (a
+// The GEMM's grid: one workgroup of four waves per CU (one wave per SIMD), each
+// wave a 128 x 128 quadrant. Modes 0-2: 4 x 4 v_mfma_f32_32x32x64_f8f6f4
+// accumulators, a block of 128 K bytes consumed as two half-steps of 16 MFMAs
+// whose operand fragments are read from LDS (16-byte reads of swizzled 128-byte
+// rows) while the previous half-step's MFMAs run. Modes 3-5: the 16 x 16 x 128
+// form the GEMM uses (k_mfma_probe16 below). The LDS stage is filled once from the caller's e4m3 codes (a
 // 256-row tile of X and one of W, at a per-workgroup offset), so the MFMAs see
 // the same operand bits a GEMM over those matrices sees, block after block.
 // mode 0: those codes; mode 1: every code e4m3 1.0 (0x38, no multiplier bits
