@@ -520,9 +520,14 @@ __device__ __forceinline__ void norm_factors(const NormArgs& p, int64_t ti, int 
 // form) at 640 and 704 chunks, where twelve fit once the next row's loads go out after
 // the row's normalization instead of before (0.0880 against 0.0907 ms with eight waves
 // and the early loads at 640; H3's 5376-wide rows, 672 chunks, as 11 per lane:
-// [13107, 5376] 0.0428 against 0.0471 ms with eight waves and 12 per lane).
+// [13107, 5376] 0.0428 against 0.0471 ms with eight waves and 12 per lane). With the late
+// loads, the next row's first kNormEarlyChunks chunks per lane still go out before the
+// normalization (the registers hold that much beside it): [13107, 5376] 41.2 against
+// 42.5 us (0, 2, 3, 4 and 6 early chunks: 42.6, 41.9, 41.3, 41.2, 41.3 us; the
+// [32760, 5120] rows 88.3 against 88.6 us).
 constexpr int norm_row_waves(int cpl, bool affine) { return cpl <= 8 || ((cpl == 10 || cpl == 11) && affine) ? 12 : 8; }
 constexpr bool norm_row_late_load(int cpl, bool affine) { return cpl > 8 && norm_row_waves(cpl, affine) == 12; }
+constexpr int kNormEarlyChunks = 4;
 // Rows in flight per wave besides the one computed (two, in the registers two waves
 // per SIMD leave at 64 chunks x 10, measured 0.0911 ms against 0.0891 ms with one).
 constexpr int norm_row_lookahead(int) { return 1; }
@@ -546,20 +551,24 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
         const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
         return (int64_t)(((uint64_t)hi << 32) | lo);
     };
-    auto load_row = [&](int64_t row, uint4 (&v)[CPL]) {
+    // chunks c0 .. c1 - 1 of a row (per lane)
+    auto load_part = [&](int64_t row, uint4 (&v)[CPL], int c0, int c1) {
         const bool valid = row < row_end;
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)uniform((int64_t)(p.x + (valid ? row : 0) * p.ldx)), 0, valid ? rowbytes : 0, 0x00020000);
 #pragma unroll
         for (int c = 0; c < CPL; ++c)
-            v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, lane16, c * kLanes * 16,
-                                                                                  kBufferLoadOnce));
+            if (c >= c0 && c < c1)
+                v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, lane16, c * kLanes * 16,
+                                                                                      kBufferLoadOnce));
     };
+    auto load_row = [&](int64_t row, uint4 (&v)[CPL]) { load_part(row, v, 0, CPL); };
     auto table_row = [&](int64_t row) -> int64_t {
         if (!AFFINE || !p.mod_index || row >= row_end) return 0;
         const int32_t ti = __builtin_amdgcn_readfirstlane(p.mod_index[row]);
         return min(max((int64_t)ti, (int64_t)0), p.mod_rows - 1);
     };
+    constexpr int kEarly = kLate ? kNormEarlyChunks : CPL;   // chunks of the next row loaded before the normalization
 
     uint4 vbuf[LA + 1][CPL];                         // buffer j: rows j, j + LA + 1, .. of this wave
 #pragma unroll
@@ -581,10 +590,8 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
 
     auto one_row = [&](int64_t row_in, uint4 (&v)[CPL], uint4 (&vn)[CPL]) {
         const int64_t row = uniform(row_in);
-        if (!kLate) {
-            load_row(row + LA * kNormRowWaves, vn);  // into the buffer the previous row freed
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        load_part(row + LA * kNormRowWaves, vn, 0, kEarly);   // into the buffer the previous row freed
+        __builtin_amdgcn_sched_barrier(0);
         const bool valid = row < row_end;
         const int64_t ti = table_row(row);
         const int slot = !valid || ti == t0 ? 0 : ti == t1 ? 1 : -1;   // wave-uniform
@@ -655,7 +662,7 @@ __global__ __launch_bounds__(norm_row_waves(CPL, AFFINE) * kLanes) void k_norm_q
         }
         if (kLate) {
             __builtin_amdgcn_sched_barrier(0);
-            load_row(row + LA * kNormRowWaves, vn);  // once the row's factors no longer hold registers
+            load_part(row + LA * kNormRowWaves, vn, kEarly, CPL);  // once the row's factors no longer hold registers
             __builtin_amdgcn_sched_barrier(0);
         }
         const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
