@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VDN_FP8_ABI_VERSION 3
+#define VDN_FP8_ABI_VERSION 4
 
 /* status codes */
 #define VDN_FP8_OK 0
@@ -48,6 +48,13 @@ extern "C" {
 #define VDN_FP8_EPI_NONE 0      /* out = v */
 #define VDN_FP8_EPI_GELU_TANH 1 /* out = 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) */
 #define VDN_FP8_EPI_GATE 2      /* out = gate[gate_index[m]][n] * v (+ residual[m][n]) */
+#define VDN_FP8_EPI_F32 3       /* out = x_scale[m] * w_scale[n] * acc, binary32 (no bias): the
+                                   scaled GEMM of a model that does not run in bf16 */
+
+/* Element types of the typed entry points (..._typed). */
+#define VDN_FP8_DTYPE_BF16 0
+#define VDN_FP8_DTYPE_F16 1
+#define VDN_FP8_DTYPE_F32 2
 
 /*
  * Per-token activation quantization: for each row m of x (bf16 [M, K]),
@@ -122,6 +129,33 @@ int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
                               void *w_merged, hipStream_t stream);
 
 /*
+ * The quantizers for rows of another float type (dtype: VDN_FP8_DTYPE_F16 or
+ * VDN_FP8_DTYPE_F32; VDN_FP8_DTYPE_BF16 forwards to the bf16 entry points above).
+ * The reference's kernels load any float type and compute in binary32; its weight
+ * branch divides in the weight's own type:
+ *   quantize_rows_typed          as vdn_fp8_quantize_rows on the binary32 values of x
+ *   swiglu_quantize_rows_typed   as vdn_fp8_swiglu_quantize_rows on those of h
+ *   requantize_weight_typed      w_scale[n] = max(max_k |w[n][k]| / 448, 1e-12),
+ *                                wq[n][k] = e4m3(T(w[n][k] / T(w_scale[n])))  (T: w's type)
+ * Codes follow torch's non-saturating cast: a quotient above 464 in magnitude
+ * (possible for binary16 weights, whose T(scale) can round far below the scale)
+ * is NaN. No LoRA here: a merge into such a weight is the reference's own update
+ * on the host side, followed by this call.
+ * Replaces: quantize_rows / swiglu_quantize, src/models/ops/fp8_linear.py:66-129
+ *           (binary16 / binary32 inputs), and the rowwise branch of
+ *           Fp8Linear.__init__, :262-267, for binary16 / binary32 weights.
+ * Requires: K % 8 == 0; row strides multiples of 8 (elements), ldx (ldh) >= K (2K),
+ *           ldy >= K; x (h, w) 16-byte and y (wq) 8-byte aligned.
+ */
+int vdn_fp8_quantize_rows_typed(const void *x, int dtype, int64_t M, int64_t K, int64_t ldx,
+                                void *y, int64_t ldy, float *scale, hipStream_t stream);
+int vdn_fp8_swiglu_quantize_rows_typed(const void *h, int dtype, int64_t M, int64_t K,
+                                       int64_t ldh, void *y, int64_t ldy, float *scale,
+                                       hipStream_t stream);
+int vdn_fp8_requantize_weight_typed(const void *w, int dtype, int64_t N, int64_t K, int64_t ldw,
+                                    void *wq, int64_t ldq, float *w_scale, hipStream_t stream);
+
+/*
  * fp8 x fp8 GEMM with per-token x per-output-channel dequantization and a
  * fused epilogue:
  *   acc[m][n] = sum_k xq[m][k] * wq[n][k]                 (fp32 accumulate)
@@ -143,6 +177,11 @@ int vdn_fp8_requantize_weight(const void *w, int64_t N, int64_t K, int64_t ldw,
  *           (torch._scaled_mm rowwise + bias add); the GELU epilogue has no
  *           reference function; the gate epilogue replaces _post_ref /
  *           the compiled `post`, src/models/ops/fused_block.py:47-49,101-110.
+ * VDN_FP8_EPI_F32 writes the binary32 x_scale[m] * w_scale[n] * acc[m][n] to
+ * out (float [M, N], row stride ldo in floats, 16-byte aligned) with bias, gate
+ * and residual NULL: the reference's _scaled_mm with out_dtype binary32 (the
+ * caller rounds to binary16 and adds the bias for the other types, as the
+ * reference does).
  * Requires: K % 16 == 0; ldx, ldw % 16 == 0; ldo, ldres, ldgate % 4 == 0;
  *           xq, wq, x_scale, w_scale, bias, gate_index 16-byte aligned;
  *           out, residual, gate 8-byte aligned.

@@ -13,6 +13,10 @@ Reference functions restated (paths relative to the reference checkout):
   quantize_rows         src/models/ops/fp8_linear.py:132-135 (quantize_rows_reference)
   swiglu_quantize_rows  src/models/ops/fp8_linear.py:83-99
   quantize_weight       src/models/ops/fp8_linear.py:262-267 (Fp8Linear.__init__, rowwise)
+  quantize_rows_float, swiglu_quantize_rows_float, quantize_weight_float
+                        the same three for float16 / float32 rows (numpy, binary32 IEEE
+                        arithmetic; the e4m3 cast is the C encoder)
+  dequant_linear_typed  forward_quantized with a float16 / float32 out_dtype
   lora_merge            src/inference/utils/lora.py:91-92 (merge_lora_state)
   dequant_linear        src/models/ops/fp8_linear.py:270-277 (forward_quantized: the
                         rowwise _scaled_mm then `out + bias`), dequantized in float64,
@@ -152,6 +156,64 @@ def quantize_weight(w):
     return q, s
 
 
+def _row_scales(xf):
+    """max(row absmax / 448, 1e-12) in binary32 with NaN propagating (torch's amax and
+    clamp_min); xf binary32 [M, K]."""
+    with np.errstate(invalid="ignore"):
+        amax = np.abs(xf).max(axis=1)          # NaN anywhere in a row -> NaN
+        s = (amax / np.float32(FP8_MAX)).astype(np.float32)
+        return np.where(s < SCALE_FLOOR, SCALE_FLOOR, s).astype(np.float32)   # NaN < x is False: NaN stays
+
+
+def quantize_rows_float(x):
+    """float16 / float32 [M, K] -> (e4m3 codes [M, K], fp32 scale [M]): quantize_rows_reference
+    (fp8_linear.py:132-135) on other float types -- x.float() / scale in binary32 (IEEE
+    division), then the cast. numpy's float32 division is the IEEE one."""
+    x = np.ascontiguousarray(x)
+    if x.dtype not in (np.float16, np.float32):
+        raise TypeError(f"expected float16 or float32 rows, got {x.dtype}")
+    xf = x.astype(np.float32)
+    s = _row_scales(xf)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        q = (xf / s[:, None]).astype(np.float32)
+    return e4m3_encode(q), s
+
+
+def swiglu_quantize_rows_float(h):
+    """float16 / float32 [M, 2K] -> (e4m3 codes [M, K], fp32 scale [M]): the reference's
+    SwiGLU quantizer (fp8_linear.py:83-99) on binary32 loads of h; sigmoid as 1 / (1 +
+    exp(-g)) in binary32 (numpy's exp: a kernel with another exp is compared within one
+    fp8 code, as for the bf16 oracle)."""
+    h = np.ascontiguousarray(h)
+    if h.dtype not in (np.float16, np.float32):
+        raise TypeError(f"expected float16 or float32 rows, got {h.dtype}")
+    hf = h.astype(np.float32)
+    K = hf.shape[1] // 2
+    a, g = hf[:, :K], hf[:, K:]
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        act = (a * g * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g)))).astype(np.float32)
+        s = _row_scales(act)
+        q = (act / s[:, None]).astype(np.float32)
+    return e4m3_encode(q), s
+
+
+def quantize_weight_float(w):
+    """float16 / float32 [N, K] -> (e4m3 codes [N, K], fp32 scale [N]): the rowwise branch
+    of Fp8Linear.__init__ (fp8_linear.py:262-267) for those types -- the scale from the
+    binary32 row maximum, then weight / scale.to(weight.dtype) in the weight's type (torch
+    divides float16 tensors in binary32 and rounds the quotient to float16), then the cast."""
+    w = np.ascontiguousarray(w)
+    if w.dtype not in (np.float16, np.float32):
+        raise TypeError(f"expected float16 or float32 rows, got {w.dtype}")
+    wf = w.astype(np.float32)
+    s = _row_scales(wf)
+    st = s.astype(w.dtype).astype(np.float32)            # scale.to(weight.dtype)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        q = (wf / st[:, None]).astype(np.float32)
+        q = q.astype(w.dtype).astype(np.float32)          # the quotient in the weight's type
+    return e4m3_encode(q), s
+
+
 def lora_merge(w, a, b, scale=1.0):
     """bf16 bits: w [N, K], a [r, K], b [N, r] -> merged w' [N, K] (bf16 bits)."""
     w, a, b = _u16(w), _u16(a), _u16(b)
@@ -179,6 +241,19 @@ def _bf16_round(v):
     """Round float64 values to bf16 (through binary32, as torch's .to(bfloat16) of a
     float32 tensor does) and return them as float64."""
     return bf16_decode(bf16_encode(np.asarray(v, np.float64).astype(np.float32))).astype(np.float64)
+
+
+def dequant_linear_typed(qx, sx, qw, sw, bias=None, out_dtype=np.float32):
+    """forward_quantized with a float16 / float32 out_dtype (fp8_linear.py:272-276): the
+    dequantized matmul in float64, rounded to out_dtype (the scaled GEMM's output), then
+    `out + bias` in that type (bias: an array of out_dtype, or None). Returns out_dtype."""
+    x = e4m3_decode(qx).astype(np.float64) * np.asarray(sx, np.float32).reshape(-1, 1).astype(np.float64)
+    w = e4m3_decode(qw).astype(np.float64) * np.asarray(sw, np.float32).reshape(-1, 1).astype(np.float64)
+    out = (x @ w.T).astype(np.float32).astype(out_dtype)
+    if bias is not None:
+        # torch adds float16 tensors in binary32 and rounds once
+        out = (out.astype(np.float32) + np.asarray(bias).astype(np.float32)[None, :]).astype(out_dtype)
+    return out
 
 
 def dequant_linear(qx, sx, qw, sw, bias=None, epilogue="none", gate=None, gate_index=None,

@@ -45,7 +45,9 @@ def test_constants_match_header():
     text = open(HEADER).read()
     for name, value in (("VDN_FP8_OK", L.OK), ("VDN_FP8_EINVAL", L.EINVAL), ("VDN_FP8_ELAUNCH", L.ELAUNCH),
                         ("VDN_FP8_EPI_NONE", L.EPI_NONE), ("VDN_FP8_EPI_GELU_TANH", L.EPI_GELU_TANH),
-                        ("VDN_FP8_EPI_GATE", L.EPI_GATE)):
+                        ("VDN_FP8_EPI_GATE", L.EPI_GATE), ("VDN_FP8_EPI_F32", L.EPI_F32),
+                        ("VDN_FP8_DTYPE_BF16", L.DTYPE_BF16), ("VDN_FP8_DTYPE_F16", L.DTYPE_F16),
+                        ("VDN_FP8_DTYPE_F32", L.DTYPE_F32)):
         assert int(re.search(rf"#define {name} (\d+)", text).group(1)) == value
 
 
@@ -89,6 +91,14 @@ FAKE = 1 << 20        # never dereferenced: every call below fails validation fi
     (lambda l: l.vdn_fp8_gated_residual(FAKE, 8, FAKE, 8, None, 0, FAKE, 8, FAKE, 8, 4, 8, None), ">= 1 row"),
     (lambda l: l.vdn_fp8_gated_residual(FAKE, 8, None, 8, None, 1, FAKE, 8, FAKE, 8, 4, 8, None), "null"),
     (lambda l: l.vdn_fp8_gated_residual(FAKE + 8, 8, FAKE, 8, None, 1, FAKE, 8, FAKE, 8, 4, 8, None), "aligned"),
+    (lambda l: l.vdn_fp8_quantize_rows_typed(FAKE, 5, 4, 8, 8, FAKE, 8, FAKE, None), "dtype"),
+    (lambda l: l.vdn_fp8_quantize_rows_typed(FAKE, 2, 4, 12, 12, FAKE, 12, FAKE, None), "multiples of 8"),
+    (lambda l: l.vdn_fp8_quantize_rows_typed(FAKE + 8, 1, 4, 8, 8, FAKE, 8, FAKE, None), "aligned"),
+    (lambda l: l.vdn_fp8_quantize_rows_typed(FAKE, 2, -1, 8, 8, FAKE, 8, FAKE, None), "negative"),
+    (lambda l: l.vdn_fp8_swiglu_quantize_rows_typed(FAKE, 2, 4, 8, 8, FAKE, 8, FAKE, None), "ldx >= 16"),
+    (lambda l: l.vdn_fp8_requantize_weight_typed(None, 1, 4, 8, 8, FAKE, 8, FAKE, None), "null"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, FAKE, 3, None, None, 0, 0, None, 0, FAKE, 4, None), "binary32"),
+    (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 3, None, None, 0, 0, None, 0, FAKE + 8, 4, None), "binary32"),
 ])
 def test_contract_violations_are_einval(call, needle):
     import vdn_fp8._lib as L
@@ -107,6 +117,10 @@ def test_empty_problems_are_no_ops():
                                           None, 8, None) == L.OK
     assert lib.vdn_fp8_qk_prep(None, 0, 2, 128, 256, None, 1e-6, None, None, 0, 0, 0, None, 256, None) == L.OK
     assert lib.vdn_fp8_gated_residual(None, 8, None, 8, None, 1, None, 8, None, 8, 0, 8, None) == L.OK
+    for dt in (L.DTYPE_F16, L.DTYPE_F32):
+        assert lib.vdn_fp8_quantize_rows_typed(None, dt, 0, 8, 8, None, 8, None, None) == L.OK
+        assert lib.vdn_fp8_swiglu_quantize_rows_typed(None, dt, 0, 8, 16, None, 8, None, None) == L.OK
+        assert lib.vdn_fp8_requantize_weight_typed(None, dt, 0, 8, 8, None, 8, None, None) == L.OK
 
 
 def test_check_raises_reference_exception_types():

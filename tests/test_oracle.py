@@ -149,6 +149,83 @@ def test_quantize_weight_matches_eager(case):
     assert np.array_equal(s.view(np.uint32), rs.reshape(-1).numpy().view(np.uint32))
 
 
+def _float_cases(dtype):
+    """Rows of float16 / float32 values: ordinary, scaled over many binades (float16 rows
+    whose scale rounds to a float16 subnormal or to zero), signed zeros, inf / NaN, and
+    values at the type's range ends."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(64, 200, generator=g) * torch.logspace(-7, 3, 64).reshape(-1, 1)
+    x[3, 5], x[4, 7], x[6, 2] = float("nan"), float("inf"), -0.0
+    x[5] = 0.0
+    yield x.to(dtype)
+    yield (torch.rand(16, 512, generator=g) * torch.finfo(dtype).max).to(dtype)
+    yield (torch.randn(8, 256, generator=g) * torch.finfo(dtype).tiny).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_quantize_rows_float_matches_eager(dtype):
+    """quantize_rows_reference on float16 / float32 rows: x.float() / scale, the cast."""
+    for x in _float_cases(dtype):
+        q, s = O.quantize_rows_float(x.numpy())
+        rq, rs = rows_reference(x)
+        assert np.array_equal(q, rq.view(torch.uint8).numpy())
+        assert np.array_equal(s.view(np.uint32), rs.reshape(-1).numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_quantize_weight_float_matches_eager(dtype):
+    """The rowwise branch of Fp8Linear.__init__ on float16 / float32 weights: the quotient
+    in the weight's own type (for float16 rows with subnormal or zero scales, quotients
+    far above 448: NaN codes, as torch's non-saturating cast gives)."""
+    nan_codes = 0
+    for w in _float_cases(dtype):
+        w = torch.nan_to_num(w, nan=1.0, posinf=2.0)
+        q, s = O.quantize_weight_float(w.numpy())
+        rq, rs = weight_reference(w)
+        assert np.array_equal(q, rq.view(torch.uint8).numpy())
+        assert np.array_equal(s.view(np.uint32), rs.reshape(-1).numpy().view(np.uint32))
+        nan_codes += int(((q & 0x7F) == 0x7F).sum())
+    if dtype == torch.float16:
+        assert nan_codes > 0          # the non-saturating cast is exercised
+
+
+def test_quantize_weight_float16_rounding_matters():
+    """A planted mistake must be caught: dividing by the binary32 scale (not its float16
+    rounding) or skipping the float16 rounding of the quotient changes codes."""
+    g = torch.Generator().manual_seed(12)
+    w = (torch.randn(64, 1024, generator=g) * 0.05).to(torch.float16)
+    rq, rs = weight_reference(w)
+    no_scale_round = (w.float() / rs.reshape(-1, 1)).to(FP8)
+    no_quot_round = (w.float() / rs.reshape(-1, 1).to(torch.float16).float()).to(FP8)
+    assert (no_scale_round.view(torch.uint8) != rq.view(torch.uint8)).any()
+    assert (no_quot_round.view(torch.uint8) != rq.view(torch.uint8)).any()
+
+
+def test_swiglu_float_oracle_close_to_eager():
+    """parity unpinned beyond tolerance, as for bf16 rows: SwiGLU + quantize on float32
+    rows against torch's eager a * g * sigmoid(g) in binary32, codes within one step."""
+    g = torch.Generator().manual_seed(13)
+    h = torch.randn(32, 2 * 384, generator=g) * 3
+    q, s = O.swiglu_quantize_rows_float(h.numpy())
+    a, gt = h[:, :384], h[:, 384:]
+    act = a * gt * torch.sigmoid(gt)
+    rs = (act.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    rq = (act / rs[:, None]).to(FP8).view(torch.uint8).numpy()
+    np.testing.assert_allclose(s, rs.numpy(), rtol=1e-6)
+    assert np.mean(q != rq) < 1e-3
+    assert np.max(np.abs(q.astype(int) - rq.astype(int))) <= 1
+
+
+def test_dequant_linear_typed_closed_form():
+    """One output by hand: codes 2.0 (0x40) and 0.5 (0x30), scales 0.25 and 4, K = 3:
+    3 * 2 * 0.5 * 0.25 * 4 = 3, plus a bias of 0.5 in float16."""
+    qx = np.full((1, 3), 0x40, np.uint8)
+    qw = np.full((1, 3), 0x30, np.uint8)
+    out = O.dequant_linear_typed(qx, [0.25], qw, [4.0], bias=np.array([0.5], np.float16), out_dtype=np.float16)
+    assert out.dtype == np.float16 and float(out[0, 0]) == 3.5
+    assert float(O.dequant_linear_typed(qx, [0.25], qw, [4.0])[0, 0]) == 3.0
+
+
 def test_quantize_weight_double_rounding_matters():
     """A planted mistake must be caught: a single rounding (binary32 quotient straight
     to e4m3, skipping the bf16 round) differs from the reference's codes on ordinary

@@ -177,7 +177,13 @@ template <int EPI>
 __device__ __forceinline__ void store4(const GemmArgs& p, int64_t m, int64_t n, const float* acc, float sxm,
                                        const uint16_t* grow)
 {
-    *reinterpret_cast<uint2*>(p.out + m * p.ldo + n) = epi4<EPI>(p, m, n, acc, sxm, grow);
+    if constexpr (EPI == VDN_FP8_EPI_F32) {   // binary32 x_scale * w_scale * acc, as tile_epilogue's
+        const float4 sw = *reinterpret_cast<const float4*>(p.sw + n);
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + m * p.ldo + n) =
+            make_float4(acc[0] * (sxm * sw.x), acc[1] * (sxm * sw.y), acc[2] * (sxm * sw.z), acc[3] * (sxm * sw.w));
+    } else {
+        *reinterpret_cast<uint2*>(p.out + m * p.ldo + n) = epi4<EPI>(p, m, n, acc, sxm, grow);
+    }
 }
 
 template <int EPI>
@@ -310,6 +316,37 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
 {
     using namespace mainloop;
     const int wn = wave & 1, wm = wave >> 1;
+    if constexpr (EPI == VDN_FP8_EPI_F32) {
+        // binary32 output x_scale * w_scale * acc, stored from the accumulators: 16 bytes
+        // (4 consecutive n of one m) per accumulator and lane; N % 4 == 0 keeps n .. n + 3
+        // inside a row whenever n is
+        uint32_t zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        const int el = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) + zero);
+        const int fr = el & 15, fg = el >> 4;
+        const float* s_sw = reinterpret_cast<const float*>(scal);
+        const float* s_sx = reinterpret_cast<const float*>(scal + 1024);
+        float* out = reinterpret_cast<float*>(p.out);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int ml = wm * 128 + 16 * j + fr;
+            const int64_t m = m0 + ml;
+            const float sxm = s_sx[ml];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int nl = wn * 128 + 16 * i + 4 * fg;
+                const int64_t n = n0 + nl;
+                const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
+                if (m < p.M && n < p.N)
+                    *reinterpret_cast<float4*>(out + m * p.ldo + n) =
+                        make_float4(acc[i][j][0] * (sxm * sw.x), acc[i][j][1] * (sxm * sw.y),
+                                    acc[i][j][2] * (sxm * sw.z), acc[i][j][3] * (sxm * sw.w));
+                acc[i][j] = f32x4_t{};   // the next tile starts from zero
+            }
+        }
+        (void)stg;
+        return;
+    }
     const bool gate16 = ((p.ldgate & 7) == 0) && (((uintptr_t)p.gate & 15) == 0);
     const bool res16 = ((p.ldres & 7) == 0) && (((uintptr_t)p.residual & 15) == 0);
     // Every lane-dependent value here derives from an opaque zero, so the
@@ -1028,6 +1065,10 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
         if (ldgate < N || ldgate % 4 || !aligned(gate, 8)) return set_error(VDN_FP8_EINVAL, "gemm: gate rows must be >= N and 8-byte aligned");
         if (residual && (ldres < N || ldres % 4 || !aligned(residual, 8)))
             return set_error(VDN_FP8_EINVAL, "gemm: residual rows must be >= N and 8-byte aligned");
+    } else if (epilogue == VDN_FP8_EPI_F32) {
+        if (bias || gate || residual || gate_index)
+            return set_error(VDN_FP8_EINVAL, "gemm: the binary32 output takes no bias, gate or residual");
+        if (!aligned(out, 16)) return set_error(VDN_FP8_EINVAL, "gemm: the binary32 output must be 16-byte aligned");
     } else if (epilogue != VDN_FP8_EPI_NONE && epilogue != VDN_FP8_EPI_GELU_TANH) {
         return set_error(VDN_FP8_EINVAL, "gemm: unknown epilogue %d", epilogue);
     }
@@ -1102,6 +1143,19 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
             hipLaunchKernelGGL((k_gemm_fp8_ktail<E>), grid, block, 0, stream, p);                        \
         }                                                                                                \
     } while (0)
+    if (epilogue == VDN_FP8_EPI_F32) {
+        // (the general epilogue only: the fast one stages bf16 rows)
+        if (main) {
+            if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_F32, false, false>), grid, block, 0, stream, p);
+            if (p.units) {
+                hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
+                hipLaunchKernelGGL((k_gemm_splitk_reduce<VDN_FP8_EPI_F32, false>), rgrid, rblock, 0, stream, p);
+            }
+        } else {
+            hipLaunchKernelGGL((k_gemm_fp8_ktail<VDN_FP8_EPI_F32>), grid, block, 0, stream, p);
+        }
+        return check_launch("gemm");
+    }
     switch (epilogue) {
         case VDN_FP8_EPI_NONE: VDN_LAUNCH(VDN_FP8_EPI_NONE); break;
         case VDN_FP8_EPI_GELU_TANH: VDN_LAUNCH(VDN_FP8_EPI_GELU_TANH); break;

@@ -254,6 +254,150 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant(
 }
 
 // ---------------------------------------------------------------------------
+// binary32 and binary16 rows (the reference's quantizers load any float type
+// and compute in binary32, fp8_linear.py:72,77,89-90; its weight branch
+// divides in the weight's own type, fp8_linear.py:264-265). A path for
+// models that do not run in bf16: one wave per row and two sweeps (the row
+// maximum, then the codes, the second reading the row again), IEEE division.
+// ---------------------------------------------------------------------------
+
+// torch's cast to e4m3fn does not saturate: a magnitude above 464 (halfway
+// between 448 and the NaN pattern) becomes NaN, as inf and NaN do.
+__device__ __forceinline__ float e4m3_domain(float q)
+{
+    return __builtin_fabsf(q) > 464.0f ? __builtin_copysignf(__builtin_nanf(""), q) : q;
+}
+
+// 16 bytes of a row as binary32 values (4 binary32 or 8 binary16 ones), and a
+// rounding to the row's own type.
+template <typename T> struct FloatRow;
+template <> struct FloatRow<float> {
+    static constexpr int kPer = 4;
+    __device__ static void unpack(uint4 v, float (&o)[8])
+    {
+        o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y);
+        o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+    }
+    __device__ static float round(float v) { return v; }
+};
+template <> struct FloatRow<_Float16> {
+    static constexpr int kPer = 8;
+    __device__ static void unpack(uint4 v, float (&o)[8])
+    {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
+            o[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
+        }
+    }
+    __device__ static float round(float v) { return (float)(_Float16)v; }
+};
+
+// The row maximum of binary32 magnitudes over the wave (NaN anywhere: NaN), then
+// the scale max(amax / 448, 1e-12) as quantize_rows forms it.
+__device__ __forceinline__ float float_row_scale(float amax, bool nan_seen)
+{
+    // non-negative binary32 patterns order like unsigned integers (NaN above inf)
+    return row_scale(__uint_as_float(wave_max_u32(nan_seen ? 0x7fc00000u : __float_as_uint(amax))));
+}
+
+// Codes of up to 8 quotients: 4 (binary32 rows) or 8 bytes at byte offset kPer c.
+template <int kPer>
+__device__ __forceinline__ void store_float_codes(uint8_t* yr, int64_t c, const float (&q)[8])
+{
+    if (kPer == 4) *reinterpret_cast<uint32_t*>(yr + 4 * c) = pack_e4m3x4(q[0], q[1], q[2], q[3]);
+    else *reinterpret_cast<uint2*>(yr + 8 * c) = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]),
+                                                            pack_e4m3x4(q[4], q[5], q[6], q[7]));
+}
+
+//   scale[m] = max(max_k |x[m][k]| / 448, 1e-12)
+//   y[m][k]  = e4m3(x[m][k] / scale[m])                    (activations)
+//   y[m][k]  = e4m3(T(x[m][k] / T(scale[m])))              (kWeight: the weight's own type)
+template <typename T, bool kWeight>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant_float(
+    const T* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    using R = FloatRow<T>;
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= M) return;
+    const int64_t nch = K / R::kPer;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    float amax = 0.0f;
+    bool nan_seen = false;
+    for (int64_t c = lane; c < nch; c += kLanes) {
+        float v[8];
+        R::unpack(xr[c], v);
+#pragma unroll
+        for (int e = 0; e < R::kPer; ++e) {
+            nan_seen |= __builtin_isnan(v[e]);
+            amax = fmaxf(amax, fabsf(v[e]));
+        }
+    }
+    const float scale = float_row_scale(amax, nan_seen);
+    if (lane == 0) scale_out[row] = scale;
+    const float sdiv = kWeight ? R::round(scale) : scale;
+    uint8_t* yr = y + row * ldy;
+    for (int64_t c = lane; c < nch; c += kLanes) {
+        float v[8], q[8];
+        R::unpack(xr[c], v);
+#pragma unroll
+        for (int e = 0; e < R::kPer; ++e) {
+            const float t = v[e] / sdiv;
+            q[e] = e4m3_domain(kWeight ? R::round(t) : t);
+        }
+        store_float_codes<R::kPer>(yr, c, q);
+    }
+}
+
+// SwiGLU + quantize of binary32 / binary16 rows h [M, 2K] (value half, then gate
+// half): act = a * g * sigmoid(g) in binary32 as k_swiglu_quant forms it, formed
+// again in the second sweep.
+template <typename T>
+__global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_float(
+    const T* __restrict__ h, int64_t M, int64_t K, int64_t ldh,
+    uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
+{
+    using R = FloatRow<T>;
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x / kLanes);
+    if (row >= M) return;
+    const int64_t nch = K / R::kPer;
+    const uint4* ar = reinterpret_cast<const uint4*>(h + row * ldh);
+    const uint4* gr = reinterpret_cast<const uint4*>(h + row * ldh + K);
+    auto acts = [&](int64_t c, float (&o)[8]) {
+        float a[8], g[8];
+        R::unpack(ar[c], a);
+        R::unpack(gr[c], g);
+#pragma unroll
+        for (int e = 0; e < R::kPer; ++e) o[e] = swiglu(a[e], g[e]);
+    };
+    float amax = 0.0f;
+    bool nan_seen = false;
+    for (int64_t c = lane; c < nch; c += kLanes) {
+        float v[8];
+        acts(c, v);
+#pragma unroll
+        for (int e = 0; e < R::kPer; ++e) {
+            nan_seen |= __builtin_isnan(v[e]);
+            amax = fmaxf(amax, fabsf(v[e]));
+        }
+    }
+    const float scale = float_row_scale(amax, nan_seen);
+    if (lane == 0) scale_out[row] = scale;
+    uint8_t* yr = y + row * ldy;
+    for (int64_t c = lane; c < nch; c += kLanes) {
+        float v[8], q[8];
+        acts(c, v);
+#pragma unroll
+        for (int e = 0; e < R::kPer; ++e) q[e] = e4m3_domain(v[e] / scale);
+        store_float_codes<R::kPer>(yr, c, q);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm + AdaLN affine + quantize
 // ---------------------------------------------------------------------------
 
@@ -1037,4 +1181,75 @@ extern "C" int vdn_fp8_requantize_weight(const void* w, int64_t N, int64_t K, in
             return set_error(VDN_FP8_ELAUNCH, "requantize_weight: copy of the merged weight failed");
     }
     return st;
+}
+
+// The typed entry points: binary16 and binary32 rows through the kernels above, bf16
+// rows through the entry points they extend.
+namespace {
+// The shared contract of a typed row call: shapes, strides, alignment, the type.
+int check_typed_rows(const char* what, const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int64_t kx,
+                     const void* y, int64_t ldy, const float* scale)
+{
+    if (dtype != VDN_FP8_DTYPE_F16 && dtype != VDN_FP8_DTYPE_F32)
+        return set_error(VDN_FP8_EINVAL, "%s: unknown dtype %d", what, dtype);
+    if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "%s: negative shape [%lld, %lld]", what, (long long)M, (long long)K);
+    if (M > 0 && K == 0) return set_error(VDN_FP8_EINVAL, "%s: K must be positive", what);
+    if (M == 0) return VDN_FP8_OK;
+    if (!x || !y || !scale) return set_error(VDN_FP8_EINVAL, "%s: null pointer", what);
+    if (K % 8 || ldx % 8 || ldy % 8 || ldx < kx || ldy < K)
+        return set_error(VDN_FP8_EINVAL, "%s: need K, the row strides multiples of 8, ldx >= %lld and ldy >= K "
+                         "(K=%lld ldx=%lld ldy=%lld)", what, (long long)kx, (long long)K, (long long)ldx, (long long)ldy);
+    if (!aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4))
+        return set_error(VDN_FP8_EINVAL, "%s: x must be 16-byte and y 8-byte aligned", what);
+    return -1;   // go on
+}
+}  // namespace
+
+extern "C" int vdn_fp8_quantize_rows_typed(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, void* y,
+                                           int64_t ldy, float* scale, hipStream_t stream)
+{
+    if (dtype == VDN_FP8_DTYPE_BF16) return vdn_fp8_quantize_rows(x, M, K, ldx, y, ldy, scale, stream);
+    const int st = check_typed_rows("quantize_rows", x, dtype, M, K, ldx, K, y, ldy, scale);
+    if (st >= 0) return st;
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    if (dtype == VDN_FP8_DTYPE_F32)
+        hipLaunchKernelGGL((k_rowquant_float<float, false>), grid, block, 0, stream, (const float*)x, M, K, ldx,
+                           (uint8_t*)y, ldy, scale);
+    else
+        hipLaunchKernelGGL((k_rowquant_float<_Float16, false>), grid, block, 0, stream, (const _Float16*)x, M, K,
+                           ldx, (uint8_t*)y, ldy, scale);
+    return check_launch("quantize_rows");
+}
+
+extern "C" int vdn_fp8_swiglu_quantize_rows_typed(const void* h, int dtype, int64_t M, int64_t K, int64_t ldh,
+                                                  void* y, int64_t ldy, float* scale, hipStream_t stream)
+{
+    if (dtype == VDN_FP8_DTYPE_BF16) return vdn_fp8_swiglu_quantize_rows(h, M, K, ldh, y, ldy, scale, stream);
+    const int st = check_typed_rows("swiglu_quantize_rows", h, dtype, M, K, ldh, 2 * K, y, ldy, scale);
+    if (st >= 0) return st;
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    if (dtype == VDN_FP8_DTYPE_F32)
+        hipLaunchKernelGGL((k_swiglu_quant_float<float>), grid, block, 0, stream, (const float*)h, M, K, ldh,
+                           (uint8_t*)y, ldy, scale);
+    else
+        hipLaunchKernelGGL((k_swiglu_quant_float<_Float16>), grid, block, 0, stream, (const _Float16*)h, M, K, ldh,
+                           (uint8_t*)y, ldy, scale);
+    return check_launch("swiglu_quantize_rows");
+}
+
+extern "C" int vdn_fp8_requantize_weight_typed(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, void* wq,
+                                               int64_t ldq, float* w_scale, hipStream_t stream)
+{
+    if (dtype == VDN_FP8_DTYPE_BF16)
+        return vdn_fp8_requantize_weight(w, N, K, ldw, nullptr, nullptr, 0, 0.0f, wq, ldq, w_scale, nullptr, stream);
+    const int st = check_typed_rows("requantize_weight", w, dtype, N, K, ldw, K, wq, ldq, w_scale);
+    if (st >= 0) return st;
+    const dim3 grid((unsigned)((N + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWavesPerBlock * kLanes);
+    if (dtype == VDN_FP8_DTYPE_F32)
+        hipLaunchKernelGGL((k_rowquant_float<float, true>), grid, block, 0, stream, (const float*)w, N, K, ldw,
+                           (uint8_t*)wq, ldq, w_scale);
+    else
+        hipLaunchKernelGGL((k_rowquant_float<_Float16, true>), grid, block, 0, stream, (const _Float16*)w, N, K, ldw,
+                           (uint8_t*)wq, ldq, w_scale);
+    return check_launch("requantize_weight");
 }

@@ -12,10 +12,11 @@ import os
 
 from .build import CSRC, INCLUDE, LIB_PATH, compiler_id, source_manifest
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, EINVAL, ELAUNCH = 0, 1, 2
-EPI_NONE, EPI_GELU_TANH, EPI_GATE = 0, 1, 2
+EPI_NONE, EPI_GELU_TANH, EPI_GATE, EPI_F32 = 0, 1, 2, 3
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 
 _lib = None
 _build_info = None
@@ -28,6 +29,9 @@ EXPORTS = (
     ("vdn_fp8_norm_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _F32, _P, _P, _I64, _P, _I64, _P, _I64, _P,
                                           _P, _I64, _P]),
     ("vdn_fp8_requantize_weight", _I32, [_P, _I64, _I64, _I64, _P, _P, _I64, _F32, _P, _I64, _P, _P, _P]),
+    ("vdn_fp8_quantize_rows_typed", _I32, [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    ("vdn_fp8_swiglu_quantize_rows_typed", _I32, [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    ("vdn_fp8_requantize_weight_typed", _I32, [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _P]),
     ("vdn_fp8_gemm", _I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P, _P, _I64, _I64,
                             _P, _I64, _P, _I64, _P]),
     ("vdn_fp8_gemm_workspace_size", _I32, [_I64, _I64, _I64, _P]),

@@ -17,6 +17,11 @@ Scale granularity. The reference picks per-tensor scales on sm100 and rowwise
 capability 9.5, so `per_tensor_gemm()` is False here and the rowwise path is the one
 implemented; the per-tensor family (quantize_tensor & co.) is not part of this module.
 
+Float types: as the reference, the quantizers take bf16, float16 or float32 rows (computed
+in binary32), Fp8Linear takes a Linear of any of the three (the weight's quotient in its own
+type), and `forward` returns the rows' type (vdn_fp8_*_typed and the GEMM's binary32
+output; the float16 cast and the bias add then follow as the reference's own ops).
+
 Extensions (keyword-only, additive): `Fp8Linear.forward_quantized` and `forward` take an
 `epilogue` ("gelu_tanh" or "gate") with `gate`, `gate_index` and `residual`, fused into
 the GEMM; `Fp8Linear(linear, lora=(A, B, scale))` quantizes W + scale * B @ A in one
@@ -58,14 +63,22 @@ def _aligned16(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def _rows(x):
-    """The reference's input check (fp8_linear.py:102-107): GPU, 2-D, then contiguous."""
+# Element types the quantizers and the GEMM's output take, with their C ABI codes. The
+# reference's Triton kernels load any float type and compute in binary32 (fp8_linear.py:72);
+# float64 is refused here (its rows would be rounded to binary32 first).
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _rows(x, dtypes=(torch.bfloat16,)):
+    """The reference's input check (fp8_linear.py:102-107): GPU, 2-D, then contiguous;
+    and an element type among `dtypes`."""
     if not x.is_cuda:
         raise ValueError("the fp8 quantiser is a HIP kernel; the input must be on the GPU")
     if x.dim() != 2:
         raise ValueError(f"expected [M, K], got {tuple(x.shape)}")
-    if x.dtype != torch.bfloat16:
-        raise ValueError(f"the fp8 quantiser takes bfloat16 input, got {x.dtype}")
+    if x.dtype not in dtypes:
+        names = ", ".join(str(d).replace("torch.", "") for d in dtypes)
+        raise ValueError(f"the fp8 quantiser takes {names} input, got {x.dtype}")
     return x.contiguous()
 
 
@@ -111,19 +124,22 @@ def check_index_range(indices, rows, what):
 
 
 def quantize_rows(x):
-    """Per-token quantization: each row of the bf16 [M, K] input is divided by its own
-    scale max(row absmax / 448, 1e-12) and cast to e4m3. Returns the codes [M, K] and
-    the binary32 scales [M, 1].
+    """Per-token quantization: each row of the [M, K] input (bf16, float16 or float32) is
+    divided by its own scale max(row absmax / 448, 1e-12), in binary32, and cast to e4m3.
+    Returns the codes [M, K] and the binary32 scales [M, 1].
 
     Codes and scales are bit-identical to `quantize_rows_reference` (the reference's
     eager spelling, fp8_linear.py:132-135). Replaces fp8_linear.py:110-117."""
-    x = _rows(x)
+    x = _rows(x, tuple(_DTYPES))
     M, K = x.shape
     y = torch.empty_like(x, dtype=FP8_DTYPE)
     scale = torch.empty(M, 1, device=x.device, dtype=torch.float32)
     lib = _lib.load()
-    _lib.check(lib.vdn_fp8_quantize_rows(_ptr(x), M, K, K, _ptr(y), K, _ptr(scale), _stream(x)),
-               "quantize_rows")
+    if x.dtype == torch.bfloat16:
+        st = lib.vdn_fp8_quantize_rows(_ptr(x), M, K, K, _ptr(y), K, _ptr(scale), _stream(x))
+    else:
+        st = lib.vdn_fp8_quantize_rows_typed(_ptr(x), _DTYPES[x.dtype], M, K, K, _ptr(y), K, _ptr(scale), _stream(x))
+    _lib.check(st, "quantize_rows")
     return y, scale
 
 
@@ -132,8 +148,9 @@ def swiglu_quantize(h):
     output [M, 2K]: its first K columns are the value a, its last K the gate g. The
     activation a * g * sigmoid(g) stays binary32 (it is never stored as bf16) and is
     quantized row by row as in `quantize_rows`; returns e4m3 [M, K] and scales [M, 1].
-    Replaces fp8_linear.py:120-129."""
-    h = _rows(h)
+    h may also be float16 or float32 (computed in binary32, as the reference's kernel
+    loads it). Replaces fp8_linear.py:120-129."""
+    h = _rows(h, tuple(_DTYPES))
     M, K2 = h.shape
     if K2 % 2:
         raise ValueError(f"swiglu_quantize needs an even width, got {K2}")
@@ -141,8 +158,12 @@ def swiglu_quantize(h):
     y = torch.empty(M, K, device=h.device, dtype=FP8_DTYPE)
     scale = torch.empty(M, 1, device=h.device, dtype=torch.float32)
     lib = _lib.load()
-    _lib.check(lib.vdn_fp8_swiglu_quantize_rows(_ptr(h), M, K, K2, _ptr(y), K, _ptr(scale), _stream(h)),
-               "swiglu_quantize")
+    if h.dtype == torch.bfloat16:
+        st = lib.vdn_fp8_swiglu_quantize_rows(_ptr(h), M, K, K2, _ptr(y), K, _ptr(scale), _stream(h))
+    else:
+        st = lib.vdn_fp8_swiglu_quantize_rows_typed(_ptr(h), _DTYPES[h.dtype], M, K, K2, _ptr(y), K, _ptr(scale),
+                                                   _stream(h))
+    _lib.check(st, "swiglu_quantize")
     return y, scale
 
 
@@ -186,8 +207,9 @@ def swiglu_quantize_activation(h):
 
 
 def requantize_weight(weight, lora=None, merged_out=None):
-    """bf16 weight [N, K] -> (fp8 codes [N, K], fp32 scale [N]) with the rowwise
-    arithmetic of Fp8Linear.__init__ (fp8_linear.py:262-267).
+    """weight [N, K] -> (fp8 codes [N, K], fp32 scale [N]) with the rowwise arithmetic of
+    Fp8Linear.__init__ (fp8_linear.py:262-267): the quotient in the weight's own type
+    (bf16, float16 or float32), then the cast.
 
     lora = (A [r, K], B [N, r], scale) folds W + bf16(scale * B @ A) in first, as
     merge_lora_state does (lora.py:91-92): with bf16 factors of rank <= 128 inside the same
@@ -197,12 +219,32 @@ def requantize_weight(weight, lora=None, merged_out=None):
     `weight` itself), receives the merged weight."""
     if not weight.is_cuda:
         raise ValueError("the fp8 requantizer is a HIP kernel; the weight must be on the GPU")
-    if weight.dim() != 2 or weight.dtype != torch.bfloat16:
-        raise ValueError(f"expected a bfloat16 [N, K] weight, got {weight.dtype} {tuple(weight.shape)}")
+    if weight.dim() != 2 or weight.dtype not in _DTYPES:
+        raise ValueError(f"expected a bfloat16, float16 or float32 [N, K] weight, got {weight.dtype} "
+                         f"{tuple(weight.shape)}")
     w = weight.contiguous()
     N, K = w.shape
     q = torch.empty(N, K, device=w.device, dtype=FP8_DTYPE)
     s = torch.empty(N, device=w.device, dtype=torch.float32)
+    if w.dtype != torch.bfloat16:
+        # float16 / float32 weights: a LoRA is merged by the reference's own update
+        # (lora.py:91-92, in the weight's type), then the typed requantization
+        if merged_out is not None and (merged_out.shape != (N, K) or merged_out.dtype != w.dtype
+                                       or not merged_out.is_contiguous() or merged_out.device != w.device):
+            raise ValueError("merged_out must be a contiguous [N, K] tensor of the weight's type and device")
+        if lora is not None:
+            a, b, lscale = lora
+            a, b = _lora_factor(a, w, "A"), _lora_factor(b, w, "B")
+            rank = a.shape[0]
+            if a.shape != (rank, K) or b.shape != (N, rank):
+                raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit a [{N}, {K}] weight")
+            w = w + lora_delta(a, b, lscale, dtype=w.dtype)
+        if merged_out is not None:
+            merged_out.copy_(w)
+        lib = _lib.load()
+        _lib.check(lib.vdn_fp8_requantize_weight_typed(_ptr(w), _DTYPES[w.dtype], N, K, K, _ptr(q), K, _ptr(s),
+                                                       _stream(w)), "requantize_weight")
+        return q, s
     a = b = None
     rank, lscale = 0, 1.0
     if merged_out is not None:
@@ -301,12 +343,16 @@ class Fp8Linear(nn.Module):
         """[M, K] fp8 rows and their [M, 1] scales -> [M, N] (fp8_linear.py:270-277).
 
         Computes bf16(epi(x_scale * w_scale * (x_fp8 @ weight_fp8.T) + bias)) in one
-        kernel. epilogue: None, "gelu_tanh", or "gate" -- gate [T, N] (or [N]) table,
+        kernel; with out_dtype float32 or float16 (a model that does not run in bf16: what
+        `forward` passes for such rows, as the reference does) the GEMM writes the binary32
+        product, then the cast and `+ bias` follow as in the reference. epilogue: None, "gelu_tanh", or "gate" -- gate [T, N] (or [N]) table,
         gate_index [M] rows of it (None = row 0; out-of-range indices are clamped),
         residual [M, N] (optional): gate[gate_index] * out + residual, the gated residual
         add of the block (fused_block.py:47-49)."""
-        if out_dtype != torch.bfloat16:
-            raise ValueError(f"the fp8 GEMM writes bfloat16 (out_dtype={out_dtype})")
+        if out_dtype not in _DTYPES:
+            raise ValueError(f"the fp8 GEMM writes bfloat16, float16 or float32 (out_dtype={out_dtype})")
+        if out_dtype != torch.bfloat16 and (epilogue is not None or gate is not None or residual is not None):
+            raise ValueError(f"the fused epilogues write bfloat16 (out_dtype={out_dtype})")
         if not x_fp8.is_cuda or x_fp8.dtype != FP8_DTYPE or x_fp8.dim() != 2:
             raise ValueError("x_fp8 must be a float8_e4m3fn [M, K] tensor on the GPU")
         M, K = x_fp8.shape
@@ -324,6 +370,24 @@ class Fp8Linear(nn.Module):
             x_fp8 = x_fp8.contiguous()
         x_fp8 = _aligned16(x_fp8)
         x_scale = _aligned16(x_scale.contiguous())
+        lib = _lib.load()
+        ws_bytes = gemm_workspace_bytes(M, N, K, dev)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+        if out_dtype != torch.bfloat16:
+            # the reference's _scaled_mm with a float16 / float32 out_dtype, then `out + bias`
+            # (fp8_linear.py:272-276): the GEMM writes the binary32 product, and the
+            # rounding to float16 and the bias add are the reference's own two ops
+            out = torch.empty(M, N, device=dev, dtype=torch.float32)
+            _lib.check(lib.vdn_fp8_gemm_ws(_ptr(x_fp8), _ptr(x_scale), _ptr(self.weight_fp8),
+                                           _ptr(self.weight_scale), M, N, K, x_fp8.stride(0), K,
+                                           None, _lib.EPI_F32, None, None, 0, 0, None, 0,
+                                           _ptr(out), N, _ptr(ws), ws_bytes, _stream(x_fp8)),
+                       "fp8 gemm")
+            if out_dtype != torch.float32:
+                out = out.to(out_dtype)
+            if self.bias is not None:
+                out = out + self.bias
+            return out
         out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
         epi = _EPILOGUES.get(epilogue)
         if epi is None:
@@ -356,9 +420,6 @@ class Fp8Linear(nn.Module):
                 ldres = res.stride(0)
         elif gate is not None or residual is not None or gate_index is not None:
             raise ValueError('gate / gate_index / residual need epilogue="gate"')
-        lib = _lib.load()
-        ws_bytes = gemm_workspace_bytes(M, N, K, dev)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
         _lib.check(lib.vdn_fp8_gemm_ws(_ptr(x_fp8), _ptr(x_scale), _ptr(self.weight_fp8),
                                        _ptr(self.weight_scale), M, N, K, x_fp8.stride(0), K,
                                        _ptr(bias), epi, _ptr(g), _ptr(gi), grows, ldgate, _ptr(res), ldres,
