@@ -975,11 +975,15 @@ void k_gemm_fp8_ktail(GemmArgs p)
 // lockstep). Measured on the QKV and FFN-down shapes; (4, 2) is as good.
 constexpr int kPhaseMod = 2, kPhaseStep = 1;
 
-// Tile order for a shape (random codes, one MI355X, [32760, N, K] of one DiT
-// block): m-tile groups of 4 with the K rotation (QKV N = 15360: 1.91 ms against
-// 1.92-1.96 for groups of 2, 8, 16 or no rotation; FFN-up N = 13824 ties with 8);
-// narrow outputs (N <= 6144, 24 n-tiles) over long rows (K >= 8192) in groups of
-// 2 (FFN-down [32760, 5120, 13824]: 1.665 ms against 1.714 with 4).
+// Tile order for a shape (random codes, one MI355X): m-tile groups of 4 with the K
+// rotation for every shape. Groups of 1, 2, 4, 8 on the 16 x 16 x 128 kernel (same
+// process, medians of three): FFN-down [32760, 5120, 13824] 1.519 / 1.505 / 1.494 /
+// 1.499 ms, attention-out [32760, 5120, 5120] 0.594 / 0.585 / 0.576 / 0.578, H3 FF
+// down [13107, 5376, 14336] 0.699 / 0.690 / 0.669 / 0.701, H3 QKV [13107, 21504, 5376]
+// 1.147 / 1.062 / 1.032 / 1.040, H3 FF projection [13107, 28672, 5376] 1.499 / 1.389 /
+// 1.369 / 1.366 (QKV N = 15360: 1.91 ms against 1.92-1.96 for 2, 8, 16 or no rotation,
+// on the earlier 32 x 32 x 64 kernel, which preferred groups of 2 for narrow outputs
+// over long rows).
 // The K rotation is on for every shape, so the summation order of an output
 // depends only on K and on the parity of its tile's (tm + tn): a projection run
 // on its own and as a row block of a fused weight (QKV's Wq;Wk;Wv, whose
@@ -990,7 +994,8 @@ __host__ inline void tile_order(int64_t N, int64_t K, int& phase_mod, int& group
 {
     phase_mod = kPhaseMod;
     group_m = kGroupM;
-    if (N <= 6144 && K >= 8192) group_m = 2;
+    (void)N;
+    (void)K;
 }
 
 // Split of the last partial round along K: for rows of at least 8192 bytes (K), when
