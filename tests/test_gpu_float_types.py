@@ -158,3 +158,20 @@ def test_float_output_refuses_the_bf16_epilogues(device):
         f.forward_quantized(qx, sx, out_dtype=torch.float32, epilogue="gelu_tanh")
     with pytest.raises(ValueError, match="float64"):
         vdn_fp8.quantize_rows(torch.randn(4, 64, device=device, dtype=torch.float64))
+
+
+def test_bf16_rows_through_a_float32_linear(device):
+    """bf16 rows into a float32 Linear: the reference's forward gives out_dtype bf16 from
+    _scaled_mm, then `out + bias` promotes to float32; the same here."""
+    lin = _linear(512, 512, torch.float32, device, seed=8)
+    f = vdn_fp8.Fp8Linear(lin)
+    x = torch.randn(64, 512, device=device).to(torch.bfloat16)
+    out = f(x)
+    assert out.dtype == torch.float32
+    qx, sx = vdn_fp8.quantize_rows(x)
+    plain = f.forward_quantized(qx, sx, out_dtype=torch.bfloat16, epilogue=None)
+    assert torch.equal(out, plain)
+    f.bias = None
+    want = f.forward_quantized(qx, sx) + lin.bias
+    assert torch.equal(out, want)
+

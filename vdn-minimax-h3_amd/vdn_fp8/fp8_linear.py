@@ -393,10 +393,19 @@ class Fp8Linear(nn.Module):
         if epi is None:
             raise ValueError(f"unknown epilogue {epilogue!r}")
         bias = self.bias
+        late_bias = None
         if bias is not None:
-            if bias.dtype != torch.bfloat16 or bias.numel() != N:
-                raise ValueError("the fused bias must be a bfloat16 [N] tensor")
-            bias = _aligned16(bias.detach().to(dev).contiguous())
+            if bias.numel() != N:
+                raise ValueError("the bias must hold one value per output channel")
+            if bias.dtype != torch.bfloat16:
+                # a bias of another type (a float32 / float16 Linear fed bf16 rows): the
+                # reference's `out + bias` promotes to that type, so it is added after the
+                # GEMM as the reference's own op (no fused epilogue then)
+                if epi != _lib.EPI_NONE:
+                    raise ValueError(f"the fused epilogues take a bfloat16 bias (got {bias.dtype})")
+                late_bias, bias = bias, None
+            else:
+                bias = _aligned16(bias.detach().to(dev).contiguous())
         g = gi = res = None
         ldgate = ldres = grows = 0
         if epi == _lib.EPI_GATE:
@@ -425,7 +434,7 @@ class Fp8Linear(nn.Module):
                                        _ptr(bias), epi, _ptr(g), _ptr(gi), grows, ldgate, _ptr(res), ldres,
                                        _ptr(out), N, _ptr(ws), ws_bytes, _stream(x_fp8)),
                    "fp8 gemm")
-        return out
+        return out if late_bias is None else out + late_bias
 
     def forward(self, x, **epilogue):
         shape = x.shape
