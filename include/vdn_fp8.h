@@ -169,10 +169,11 @@ int vdn_fp8_requantize_weight_typed(const void *w, int dtype, int64_t N, int64_t
  * bias bf16 [N] or NULL. For VDN_FP8_EPI_GATE: gate bf16 [gate_rows, N] (row
  * stride ldgate), gate_index int32 [M] (NULL = row 0 for every m; an index
  * outside [0, gate_rows) is clamped into it), residual bf16 [M, N] (row stride
- * ldres) or NULL. out bf16 [M, N] (row stride ldo). With a per-row gate or a
- * residual and 16-byte aligned rows the call runs two kernels on the stream
- * (the GEMM writing v, then the gated residual add in place on out); the
- * result is the same.
+ * ldres) or NULL. out bf16 [M, N] (row stride ldo). A per-row gate or a
+ * residual on 16-byte aligned rows applies in the GEMM's epilogue; on other
+ * rows, or rows whose byte offsets within 256 rows exceed 31 bits, the call
+ * runs two kernels on the stream (the GEMM writing v, then the gated residual
+ * add in place on out). The result is the same.
  * Replaces: Fp8Linear.forward_quantized, src/models/ops/fp8_linear.py:270-277
  *           (torch._scaled_mm rowwise + bias add); the GELU epilogue has no
  *           reference function; the gate epilogue replaces _post_ref /

@@ -554,3 +554,43 @@ def test_gemm_split_k(device, M, N, K, epi):
     import vdn_fp8._lib as L
     with pytest.raises(ValueError, match="workspace"):
         _raw_gemm(f, qx, sx, o_split, ws[:ws.numel() - 16], **raw)
+
+
+@pytest.mark.parametrize("M,N,K,T,order,bias,res", [
+    (13107, 5376, 14336, 5, "frames", False, True),   # H3 FF down: split-K tiles through the reduction
+    (1000, 1032, 1024, 4, "random", True, True),      # partial tiles in M and N, out-of-range indices
+    (777, 2048, 8192, 3, "random", False, False),     # split, per-row gate without a residual
+    (300, 512, 5120, 1, "frames", True, True),        # one-row table with a residual
+])
+def test_gemm_row_gate_epilogue_matches_two_kernels(device, M, N, K, T, order, bias, res):
+    """The per-row gate and the residual applied in the GEMM's fast epilogue, bit for bit the
+    GEMM writing v followed by the gated residual kernel on it (vdn_fp8_gated_residual, the
+    compiled `post` of fused_block.py:47-49): the same two roundings in the same order, so the
+    fused form may not move a bit. Table indices frame-ordered (the model's) or random with
+    values outside the table (clamped, as the gated residual kernel clamps)."""
+    import vdn_fp8._lib as L
+    print(f"row-gate epilogue [{M}, {N}, {K}] T={T} {order} bias={bias} residual={res}", flush=True)
+    g = torch.Generator(device=device).manual_seed(M + N)
+    lin = torch.nn.Linear(K, N, bias=bias, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(0.02 * torch.randn(N, K, device=device, generator=g))
+        if bias:
+            lin.bias.copy_(0.1 * torch.randn(N, device=device, generator=g))
+    f = vdn_fp8.Fp8Linear(lin)
+    qx, sx = vdn_fp8.quantize_rows(torch.randn(M, K, device=device, generator=g).to(torch.bfloat16))
+    gate = (2 * torch.rand(T, N, device=device, generator=g) - 1).to(torch.bfloat16)
+    gate[0, :8] = -0.0                                  # -0 gates keep the product's sign
+    if order == "frames":
+        gi = (torch.arange(M, device=device) * T // M).to(torch.int32)
+    else:
+        gi = torch.randint(-1, T + 1, (M,), device=device, generator=g, dtype=torch.int32)
+    resid = torch.randn(M, N, device=device, generator=g).to(torch.bfloat16) if res else None
+    fused = f.forward_quantized(qx, sx, epilogue="gate", gate=gate, gate_index=gi, residual=resid)
+    v = f.forward_quantized(qx, sx)
+    two = torch.empty_like(v)
+    st = torch.cuda.current_stream().cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()
+    L.check(L.load().vdn_fp8_gated_residual(ptr(resid), N, ptr(gate), N, ptr(gi), T, ptr(v), N, ptr(two), N, M, N, st),
+            "gated_residual")
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16))

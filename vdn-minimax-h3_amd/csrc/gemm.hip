@@ -35,9 +35,8 @@
 // epilogue stores 8 bytes (4 bf16) per lane.
 //
 // Tile order: workgroup b runs on XCD b % 8; tiles are renumbered so each XCD
-// walks a contiguous run of the tile space, grouped kGroupM (4) m-tiles at a time
-// (2 for narrow outputs over long rows), which keeps the X and W slices its 32 CUs
-// share resident in that XCD's L2.
+// walks a contiguous run of the tile space, grouped kGroupM (4) m-tiles at a time,
+// which keeps the X and W slices its 32 CUs share resident in that XCD's L2.
 //
 // K % 128 != 0 goes to a second kernel (BK = 128, 16x16x128 MFMA, two stages)
 // whose last step is filled through VGPRs with zeros past K.
@@ -63,6 +62,11 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Internal epilogue (not an ABI value): VDN_FP8_EPI_GATE with a per-row gate index
+// and/or a residual, on 16-byte rows -- the fast epilogue with the gate and the residual
+// applied in the staging's row layout.
+constexpr int kEpiRowGate = 4;
 
 struct GemmArgs {
     const uint8_t* xq;
@@ -309,8 +313,9 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // apply in that row layout.
 // scal: the tile's vectors (4 KiB: w_scale, x_scale, bias, gate index or gate row, 1 KiB
 // each); stg: this wave's staging rows. Shared by the main kernel and the split-K
-// reduction.
-template <int EPI, bool FAST>
+// reduction. U >= 0: only the quadrant's rows 32 U .. 32 U + 31 (the reduction's four
+// waves share a quadrant's epilogue).
+template <int EPI, bool FAST, int U = -1>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* scal, uint8_t* stg,
                                               f32x4_t (&acc)[8][8], int64_t m0, int64_t n0, int wave)
 {
@@ -329,6 +334,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
         float* out = reinterpret_cast<float*>(p.out);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
+            if (U >= 0 && (j >> 1) != U) continue;
             const int ml = wm * 128 + 16 * j + fr;
             const int64_t m = m0 + ml;
             const float sxm = s_sx[ml];
@@ -456,7 +462,54 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
         for (int i = 0; i < 4; ++i) pv[i] = *reinterpret_cast<const uint4*>(stg + (8 * i + rl) * kStgRow + (cc << 4));
     };
     // (the four offsets first, then the four stores back to back and their wait states)
-    auto store_slab = [&](int th, int u) {
+    // Row gate: the gate table row gate_index[m] and the residual for the slab's rows
+    // 8 i + L/8, columns 8 (L % 8) .. + 7 of the column half, by 16-byte buffer loads
+    // issued two slabs ahead of their use into one of two register sets (rows past M and
+    // columns past N read outside the descriptors: zeros), then, in the stores' row
+    // layout, out = bf16(residual + gate * v) -- the gated residual kernel's arithmetic.
+    constexpr bool kRowGate = EPI == kEpiRowGate;
+    const bool has_res = p.residual != nullptr;
+    const int64_t rows_here = min(p.M - m0, (int64_t)BM);
+    const __amdgpu_buffer_rsrc_t rsr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kRowGate && has_res ? p.residual + m0 * p.ldres : nullptr), 0,
+        kRowGate && has_res ? (int)(((rows_here - 1) * p.ldres + p.N) * 2) : 0, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t gsr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kRowGate ? p.gate : nullptr), 0, kRowGate ? (int)(((p.gate_rows - 1) * p.ldgate + p.N) * 2) : 0,
+        kRsrcWord3);
+    uint4 rres[2][4], rgat[2][4];
+    auto load_rows = [&](int th, int u, int set) {
+        const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
+        const bool nin = n < p.N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ml = wm * 128 + 32 * u + 8 * i + rl;
+            const int64_t gi = min(max((int64_t)s_gi[ml], (int64_t)0), p.gate_rows - 1);
+            const uint32_t ro = nin ? (uint32_t)(((int64_t)ml * p.ldres + n) * 2) : 0x80000000u;
+            const uint32_t go = nin ? (uint32_t)((gi * p.ldgate + n) * 2) : 0x80000000u;
+            rres[set][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsr, ro, 0, kBufferLoadOnce));
+            rgat[set][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(gsr, go, 0, 0));
+        }
+    };
+    auto apply_rows = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t vw[4] = {pv[i].x, pv[i].y, pv[i].z, pv[i].w};
+            const uint32_t gw[4] = {rgat[set][i].x, rgat[set][i].y, rgat[set][i].z, rgat[set][i].w};
+            const uint32_t rw[4] = {rres[set][i].x, rres[set][i].y, rres[set][i].z, rres[set][i].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // without a residual the product is stored as it is (no + 0: -0 stays -0)
+                float lo = bf16_lo(gw[e]) * bf16_lo(vw[e]);
+                float hi = bf16_hi(gw[e]) * bf16_hi(vw[e]);
+                if (has_res) { lo = bf16_lo(rw[e]) + lo; hi = bf16_hi(rw[e]) + hi; }
+                o[e] = pack_bf16x2(lo, hi);
+            }
+            pv[i] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    };
+    auto store_slab = [&](int th, int u, int set) {
+        if constexpr (kRowGate) apply_rows(set);
         const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
         const uint32_t off0 = (uint32_t)(wm * 128 + 32 * u + rl) * ldo2 + (uint32_t)(n * 2);
         uint32_t off[4];
@@ -468,15 +521,25 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off[i], 0, kStoreNT);
         settle_stores();
     };
+    // (U >= 0: only the slabs of rows 32 U .. 32 U + 31, sidx = 3 - U and 7 - U)
+    constexpr int kFirst = U < 0 ? 0 : 3 - U;
+    constexpr int kStep = U < 0 ? 1 : 4, kLast = U < 0 ? 7 : 7 - U;
+    // (the register set of slab sidx: the parity of its place in the order)
+    auto set_of = [](int sidx) { return ((sidx - kFirst) / kStep) & 1; };
+    if constexpr (kRowGate) load_rows(1 - kFirst / 4, 3 - kFirst % 4, 0);
 #pragma unroll
     for (int sidx = 0; sidx < 8; ++sidx) {
         const int th = 1 - sidx / 4, u = 3 - sidx % 4;
-        if (sidx % 4 == 0) hoist(th);
-        if (FAST && sidx > 0) read_slab();   // the previous slab, before this one overwrites it
+        if (U >= 0 && u != U) continue;
+        if (U >= 0 || sidx % 4 == 0) hoist(th);
+        if (FAST && sidx > kFirst) read_slab();   // the previous slab, before this one overwrites it
         if (has_bias) compute(th, u, std::true_type{});
         else compute(th, u, std::false_type{});
         if (FAST) {
-            if (sidx > 0) store_slab(1 - (sidx - 1) / 4, 3 - (sidx - 1) % 4);
+            if (sidx > kFirst) store_slab(1 - (sidx - kStep) / 4, 3 - (sidx - kStep) % 4, set_of(sidx - kStep));
+            if constexpr (kRowGate) {
+                if (sidx < kLast) load_rows(1 - (sidx + kStep) / 4, 3 - (sidx + kStep) % 4, set_of(sidx + kStep));
+            }
         } else {
             const int64_t n = n0 + wn * 128 + 64 * th + 8 * cc;
             const bool full = n + 8 <= p.N;
@@ -526,9 +589,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
         // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (FAST) {   // the last slab (th 0, u 0)
+    if (FAST) {   // the last slab (th 0, u 0; u U)
         read_slab();
-        store_slab(0, 0);
+        store_slab(0, U < 0 ? 0 : U, set_of(kLast));
     }
 }
 
@@ -540,12 +603,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
 // two scalar buffers at the start of the tile before, one copy per wave. The
 // epilogue stages through LDS of its own.
 //
-// FAST (16-byte aligned output rows; no per-row gate and no residual -- a
-// broadcast gate row travels with the tile's vectors): the epilogue issues
-// exactly kEpiStores buffer stores per wave, columns past N sent out of range
-// (dropped), so the waits that follow count them and the stores drain while
-// the next tile runs. Otherwise the waits also cover the epilogue's memory
-// operations.
+// FAST (16-byte aligned output rows; a broadcast gate row travels with the tile's
+// vectors, a per-row gate and the residual -- kEpiRowGate -- are loaded by the
+// epilogue two slabs ahead of their use): the epilogue issues exactly kEpiStores
+// buffer stores per wave, columns past N sent out of range (dropped), and every
+// load it issues has landed when it ends, so the waits that follow count the
+// stores (conservatively, the counter retiring in issue order) and the stores
+// drain while the next tile runs. Otherwise the waits also cover the epilogue's
+// memory operations.
 // PARTIAL: the split units instead of the whole tiles (one per workgroup, its K slice,
 // the partial sums stored raw; a launch of its own, so that the whole-tile kernel keeps
 // one straight-line epilogue; EPI and FAST do not matter to it: one instance serves).
@@ -805,26 +870,29 @@ void k_gemm_fp8(GemmArgs p)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 }
 
-// Split-K reduction: one single-wave workgroup per quadrant of a split tile (four per
-// tile, one wave per SIMD). The wave sums its accumulators' partial sums over the tile's
-// units in slice order (slice 0 + slice 1 + ..., binary32: the order depends only on K and
-// the split), each slice's 64 KiB read by 64 loads in flight at once, stages the tile's
-// vectors as the main kernel's copies lay them out, and runs the same epilogue for its
-// quadrant.
+// Split-K reduction: one workgroup of four waves per quadrant of a split tile (four per
+// tile). Wave w sums accumulators 16 w .. 16 w + 15 of the quadrant (per lane) over the
+// tile's units in slice order (slice 0 + slice 1 + ..., binary32: the order depends only
+// on K and the split), two slices' loads in flight at once beside the sums, into LDS; wave
+// 3 stages the tile's vectors as the main kernel's copies lay them out; then each wave
+// runs the same epilogue for the quadrant's rows 32 w .. 32 w + 31 (its two slabs). Against
+// one wave per quadrant holding all 64 accumulators: [3328, 5120, 8192] 0.124 -> 0.113 ms,
+// [1000, 1000, 16384] 0.059 -> 0.042 ms, bitwise equal.
 template <int EPI, bool FAST>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm_splitk_reduce(GemmArgs p)
 {
     using namespace mainloop;
     __shared__ __attribute__((aligned(1024))) uint8_t scal[4096];
-    __shared__ __attribute__((aligned(16))) uint8_t stg[kStgWave];
-    const int lane = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) uint8_t stg[4 * kStgWave];
+    __shared__ f32x4_t sums[64 * 64];   // [accumulator][lane]
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int quad = blockIdx.x & 3, r = blockIdx.x >> 2;
     int tm, tn;
     tile_coords(p.t_main + r, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     // (branch-free buffer loads, all in flight at once: entries past N or M read as zeros)
-    {
+    if (w == 3) {
         const int64_t nn = min(p.N - n0, (int64_t)256), mm = min(p.M - m0, (int64_t)256);
         const __amdgpu_buffer_rsrc_t swr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sw + n0), 0, (int)(nn * 4), kRsrcWord3);
         const __amdgpu_buffer_rsrc_t sxr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sx + m0), 0, (int)(mm * 4), kRsrcWord3);
@@ -850,31 +918,45 @@ void k_gemm_splitk_reduce(GemmArgs p)
         (void*)(p.ws + (int64_t)r * p.splits * kUnitFloatsDev + (int64_t)quad * 16384), 0,
         (int)min((int64_t)p.splits * kUnitFloatsDev * 4, (int64_t)0x7fffffff), kRsrcWord3);
     const uint32_t l16 = (uint32_t)lane * 16;
-    // (the later slices in batches of 32 loads, each batch in flight at once: the
-    // registers hold the sums and one batch)
-    f32x4_t a[64], b[32];
+    const int i0 = 16 * w;   // this wave's accumulators i0 .. i0 + 15
+    f32x4_t a[16];
 #pragma unroll
-    for (int i = 0; i < 64; ++i)
-        a[i] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, i * 1024, 0));
-    for (int sl = 1; sl < p.splits; ++sl) {
-        const int so = sl * (int)kUnitFloatsDev * 4;
+    for (int q = 0; q < 16; ++q)
+        a[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, (i0 + q) * 1024, 0));
+    for (int sl = 1; sl < p.splits; sl += 2) {
+        const bool two = sl + 1 < p.splits;
+        // (a missing second slice is read past the descriptor's range: zeros, no traffic)
+        const int so = sl * (int)kUnitFloatsDev * 4, so2 = so + (int)kUnitFloatsDev * 4;
+        f32x4_t b[16], c[16];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
+        for (int q = 0; q < 16; ++q)
+            b[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, so + (i0 + q) * 1024, 0));
 #pragma unroll
-            for (int i = 0; i < 32; ++i)
-                b[i] = __builtin_bit_cast(f32x4_t,
-                                          __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, so + (32 * c + i) * 1024, 0));
-            __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < 16; ++q)
+            c[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wsr, l16, so2 + (i0 + q) * 1024, 0));
 #pragma unroll
-            for (int i = 0; i < 32; ++i) a[32 * c + i] += b[i];
-            __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < 16; ++q) a[q] += b[q];
+        if (two) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) a[q] += c[q];
         }
     }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sums[(i0 + q) * 64 + lane] = a[q];
+    __syncthreads();
+    // wave w: the epilogue's slabs of rows 32 w .. 32 w + 31 (accumulators [.][2 w], [.][2 w + 1])
     f32x4_t acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) acc[i >> 3][i & 7] = a[i];
-    __syncthreads();
-    tile_epilogue<EPI, FAST>(p, scal, stg, acc, m0, n0, quad);
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = sums[(8 * i + j) * 64 + lane];
+    uint8_t* const ws = stg + w * kStgWave;
+    switch (w) {
+        case 0: tile_epilogue<EPI, FAST, 0>(p, scal, ws, acc, m0, n0, quad); break;
+        case 1: tile_epilogue<EPI, FAST, 1>(p, scal, ws, acc, m0, n0, quad); break;
+        case 2: tile_epilogue<EPI, FAST, 2>(p, scal, ws, acc, m0, n0, quad); break;
+        default: tile_epilogue<EPI, FAST, 3>(p, scal, ws, acc, m0, n0, quad); break;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1108,18 +1190,31 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
     }
     const dim3 grid((unsigned)std::max<int64_t>(blocks, 1)), block(kThreads);
     const dim3 ugrid((unsigned)std::max(p.units, 1)), rgrid((unsigned)(p.units ? 4 * (p.units / p.splits) : 1));
-    const dim3 rblock(64);
+    const dim3 rblock(256);
     // the fast epilogue: 16-byte output rows, row offsets within 31 bits, and no
     // per-row gate or residual (a gate table of one row is staged like the bias)
     const bool gate_broadcast = epilogue == VDN_FP8_EPI_GATE && !residual && (gate_rows == 1 || !gate_index) &&
                                 aligned(gate, 16);
     const bool out16 = N % 8 == 0 && ldo % 8 == 0 && aligned(out, 16) && (int64_t)BM * ldo * 2 <= (int64_t)0x7fffffff;
     const bool fast = (epilogue != VDN_FP8_EPI_GATE || gate_broadcast) && out16;
-    // A per-row gate or a residual on 16-byte rows: the fast GEMM writes v, then the
-    // gated residual kernel forms bf16(residual + gate[i] * v) in place -- the same
-    // two roundings as the epilogue, without its per-row loads inside the GEMM.
-    if (main && epilogue == VDN_FP8_EPI_GATE && !gate_broadcast && out16 && aligned(gate, 16) && ldgate % 8 == 0 &&
-        (!residual || (aligned(residual, 16) && ldres % 8 == 0))) {
+    // A per-row gate or a residual on 16-byte rows: the fast epilogue with the gate and
+    // the residual applied in its row layout, bf16(residual + gate[i] * v), the gated
+    // residual kernel's arithmetic (H3 FF down [13107, 5376, 14336] with a gate table
+    // and the residual: 0.750 -> 0.691 ms against the GEMM writing v and that kernel
+    // reading it back; [32760, 5120, 13824] 1.628 -> 1.532 ms; bitwise equal). Row
+    // offsets past 31 bits keep the two kernels.
+    const bool row_gate = main && epilogue == VDN_FP8_EPI_GATE && !gate_broadcast && out16 && aligned(gate, 16) &&
+                          ldgate % 8 == 0 && (!residual || (aligned(residual, 16) && ldres % 8 == 0));
+    if (row_gate && (!residual || (int64_t)BM * ldres * 2 <= (int64_t)0x7fffffff) &&
+        gate_rows * ldgate * 2 <= (int64_t)0x7fffffff) {
+        if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<kEpiRowGate, true, false>), grid, block, 0, stream, p);
+        if (p.units) {
+            hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
+            hipLaunchKernelGGL((k_gemm_splitk_reduce<kEpiRowGate, true>), rgrid, rblock, 0, stream, p);
+        }
+        return check_launch("gemm");
+    }
+    if (row_gate) {
         if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, false>), grid, block, 0, stream, p);
         if (p.units) {
             hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
