@@ -33,8 +33,9 @@ def _randn_bits(rng, M, K, std=1.0):
     return O.bf16_encode(rng.standard_normal((M, K), dtype=np.float32) * std)
 
 
-@pytest.mark.parametrize("M,K", [(1, 8), (3, 24), (5, 512), (64, 1024), (17, 5120), (9, 5376),
-                                 (33, 13824), (4, 14336), (6, 16384), (3, 16392), (2, 40000)])
+@pytest.mark.parametrize("M,K", [(1, 8), (3, 24), (5, 512), (64, 1024), (3, 4096), (7, 4104), (17, 5120),
+                                 (9, 5376), (5, 8192), (2, 8200), (33, 13824), (4, 14336), (6, 16384), (3, 16392),
+                                 (2, 40000)])
 def test_quantize_rows_shapes(device, M, K):
     print(f"quantize_rows M={M} K={K}", flush=True)
     rng = np.random.default_rng(M * 100003 + K)

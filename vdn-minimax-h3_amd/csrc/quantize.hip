@@ -92,9 +92,9 @@ __device__ __forceinline__ uint2 quantize_chunk(uint4 v, float s, float r)
 // WPR waves share a row (1, 2 or 4); CPL = 16-byte chunks held per lane, with
 // CPL*64*WPR >= K/8. Wave part p of a row holds chunks p*64 + lane + 64*WPR*c,
 // so the waves of a row read interleaved 1 KiB blocks; their row maxima meet in
-// LDS. Two waves per row halve the registers per wave and double the
-// workgroups: [32760, 5120] activations in 0.075 ms against 0.077 ms with one
-// (non-temporal loads in both).
+// LDS. More waves per row cut the registers per wave and multiply the
+// workgroups: [32760, 5120] activations in 0.075 ms with two against 0.077 ms with
+// one (non-temporal loads in both), 76.3 against 77.3 us with four against two.
 template <int CPL, bool kWeight, int WPR, bool NT>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
@@ -916,9 +916,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
     }
 }
 
-// Rows of 4096..16384 elements: two waves per row up to 8192 elements, four
-// beyond (chunks per lane rounded up to an instantiated CPL). Returns false for
-// other widths.
+// Rows of 4096..16384 elements: four waves per row (chunks per lane rounded up to
+// an instantiated CPL; [32760, 13824]: 0.224 ms against 0.229 ms with two; [32760,
+// 5120] 76.3 against 77.3 us, the [15360, 5120] weight 39.4 against 39.9 us).
+// Returns false for other widths.
 template <bool kWeight, bool NT>
 bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
                           uint8_t* y, int64_t ldy, float* s)
@@ -926,28 +927,14 @@ bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t 
     const int64_t nch = K / 8;
     if (nch < 8 * kLanes || nch > 2 * 16 * kLanes) return false;
     const dim3 block(kWavesPerBlock * kLanes);
-    if (nch > 16 * kLanes) {
-        // rows of more than 8192 elements: four waves per row ([32760, 13824]:
-        // 0.224 ms against 0.229 ms with two)
-        const int64_t per = (nch + 4 * kLanes - 1) / (4 * kLanes);     // chunks per lane
-        const dim3 grid((unsigned)M);
-#define VDN_CASE(n)                                                                                    \
-        if (per <= n) {                                                                                \
-            hipLaunchKernelGGL((k_rowquant<n, kWeight, 4, NT>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
-            return true;                                                                               \
-        }
-        VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
-#undef VDN_CASE
-        return false;
-    }
-    const int64_t per = (nch + 2 * kLanes - 1) / (2 * kLanes);     // chunks per lane
-    const dim3 grid((unsigned)((M + 1) / 2));
+    const int64_t per = (nch + 4 * kLanes - 1) / (4 * kLanes);     // chunks per lane
+    const dim3 grid((unsigned)M);
 #define VDN_CASE(n)                                                                                    \
     if (per <= n) {                                                                                    \
-        hipLaunchKernelGGL((k_rowquant<n, kWeight, 2, NT>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        hipLaunchKernelGGL((k_rowquant<n, kWeight, 4, NT>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
         return true;                                                                                   \
     }
-    VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
+    VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
 #undef VDN_CASE
     return false;
 }
