@@ -594,3 +594,30 @@ def test_gemm_row_gate_epilogue_matches_two_kernels(device, M, N, K, T, order, b
             "gated_residual")
     torch.cuda.synchronize()
     assert torch.equal(fused.view(torch.int16), two.view(torch.int16))
+
+
+@pytest.mark.parametrize("epi", [None, "gelu_tanh"])
+def test_gemm_quadrant_tiles_match_whole_tiles(device, epi):
+    """A shape of few tiles runs them as quadrants (four workgroups per 256 x 256 tile, each
+    wave 64 x 64 of it); the same rows and columns inside a shape that fills a whole round
+    of the persistent kernel come out bit for bit the same: every output is the same chain
+    of MFMAs over the same K blocks, in its tile's rotated order, then the same epilogue."""
+    M, K, N, N2 = 1000, 2048, 520, 16384    # 4 x 3 tiles (quadrants); 4 x 64 = 256 tiles (whole tiles)
+    print(f"quadrant tiles [{M}, {N}, {K}] against [{M}, {N2}, {K}], epilogue {epi}", flush=True)
+    g = torch.Generator(device=device).manual_seed(41)
+    lin = torch.nn.Linear(K, N2, bias=True, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(0.02 * torch.randn(N2, K, device=device, generator=g))
+        lin.bias.copy_(0.1 * torch.randn(N2, device=device, generator=g))
+    small = torch.nn.Linear(K, N, bias=True, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        small.weight.copy_(lin.weight[:N])
+        small.bias.copy_(lin.bias[:N])
+    big_f, small_f = vdn_fp8.Fp8Linear(lin), vdn_fp8.Fp8Linear(small)
+    assert torch.equal(small_f.weight_fp8.view(torch.uint8), big_f.weight_fp8.view(torch.uint8)[:N])
+    qx, sx = vdn_fp8.quantize_rows(torch.randn(M, K, device=device, generator=g).to(torch.bfloat16))
+    kw = {} if epi is None else {"epilogue": epi}
+    a = small_f.forward_quantized(qx, sx, **kw)
+    b = big_f.forward_quantized(qx, sx, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b[:, :N].view(torch.int16))

@@ -311,11 +311,17 @@ __device__ __forceinline__ i32x4_t rsrc_words(const void* base, int64_t bytes)
 // back by rows and stores 16-byte pieces of whole 128-byte row segments: lane
 // L covers row 8 i + L/8, channels 8 (L%8) .. +7. The gate and residual
 // apply in that row layout.
+// The epilogue's slabs in order: sidx = 4 (1 - th) + 3 - u, (th, u) = (1, 3), (1, 2), ..
+// (0, 0). A slab mask (bit sidx; -1: every slab) restricts an epilogue to some of them.
+constexpr bool slab_in(int mask, int s) { return mask < 0 || ((mask >> s) & 1); }
+constexpr int slab_first(int mask) { return mask < 0 ? 0 : __builtin_ctz((unsigned)mask); }
+constexpr int slab_last(int mask) { return mask < 0 ? 7 : 31 - __builtin_clz((unsigned)mask); }
+
 // scal: the tile's vectors (4 KiB: w_scale, x_scale, bias, gate index or gate row, 1 KiB
-// each); stg: this wave's staging rows. Shared by the main kernel and the split-K
-// reduction. U >= 0: only the quadrant's rows 32 U .. 32 U + 31 (the reduction's four
-// waves share a quadrant's epilogue).
-template <int EPI, bool FAST, int U = -1>
+// each); stg: this wave's staging rows. Shared by the main kernel, the split-K reduction
+// (four waves on a quadrant, each its 32 rows) and the quadrant kernel (each wave 64 x
+// 64): MASK >= 0 restricts the epilogue to those slabs (bit sidx).
+template <int EPI, bool FAST, int MASK = -1>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* scal, uint8_t* stg,
                                               f32x4_t (&acc)[8][8], int64_t m0, int64_t n0, int wave)
 {
@@ -334,12 +340,12 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
         float* out = reinterpret_cast<float*>(p.out);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            if (U >= 0 && (j >> 1) != U) continue;
             const int ml = wm * 128 + 16 * j + fr;
             const int64_t m = m0 + ml;
             const float sxm = s_sx[ml];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
+                if (!slab_in(MASK, 4 * (1 - (i >> 2)) + 3 - (j >> 1))) continue;
                 const int nl = wn * 128 + 16 * i + 4 * fg;
                 const int64_t n = n0 + nl;
                 const float4 sw = *reinterpret_cast<const float4*>(s_sw + nl);
@@ -521,17 +527,18 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, pv[i]), orr, off[i], 0, kStoreNT);
         settle_stores();
     };
-    // (U >= 0: only the slabs of rows 32 U .. 32 U + 31, sidx = 3 - U and 7 - U)
-    constexpr int kFirst = U < 0 ? 0 : 3 - U;
-    constexpr int kStep = U < 0 ? 1 : 4, kLast = U < 0 ? 7 : 7 - U;
+    // (MASK >= 0: two slabs, kFirst and kLast)
+    static_assert(MASK < 0 || __builtin_popcount((unsigned)MASK) == 2, "a slab mask holds two slabs");
+    constexpr int kFirst = slab_first(MASK), kLast = slab_last(MASK);
+    constexpr int kStep = MASK < 0 ? 1 : kLast - kFirst;
     // (the register set of slab sidx: the parity of its place in the order)
     auto set_of = [](int sidx) { return ((sidx - kFirst) / kStep) & 1; };
     if constexpr (kRowGate) load_rows(1 - kFirst / 4, 3 - kFirst % 4, 0);
 #pragma unroll
     for (int sidx = 0; sidx < 8; ++sidx) {
         const int th = 1 - sidx / 4, u = 3 - sidx % 4;
-        if (U >= 0 && u != U) continue;
-        if (U >= 0 || sidx % 4 == 0) hoist(th);
+        if (MASK >= 0 && !((MASK >> sidx) & 1)) continue;
+        if (MASK >= 0 || sidx % 4 == 0) hoist(th);
         if (FAST && sidx > kFirst) read_slab();   // the previous slab, before this one overwrites it
         if (has_bias) compute(th, u, std::true_type{});
         else compute(th, u, std::false_type{});
@@ -589,9 +596,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const uint8_t* 
         // one slab at a time: unbounded interleaving of slabs runs out of VGPRs
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (FAST) {   // the last slab (th 0, u 0; u U)
+    if (FAST) {   // the last slab
         read_slab();
-        store_slab(0, U < 0 ? 0 : U, set_of(kLast));
+        store_slab(1 - kLast / 4, 3 - kLast % 4, set_of(kLast));
     }
 }
 
@@ -870,6 +877,151 @@ void k_gemm_fp8(GemmArgs p)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 }
 
+// The tile's vectors at (m0, n0) staged in LDS as the main kernel's copies lay them out
+// (w_scale, x_scale, bias, then the broadcast gate row or gate_index), by one wave:
+// branch-free buffer loads, all in flight at once; entries past N or M read as zeros.
+template <int EPI, bool FAST>
+__device__ __forceinline__ void stage_tile_vectors(const GemmArgs& p, uint8_t* scal, int64_t m0, int64_t n0, int lane)
+{
+    const int64_t nn = min(p.N - n0, (int64_t)256), mm = min(p.M - m0, (int64_t)256);
+    const __amdgpu_buffer_rsrc_t swr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sw + n0), 0, (int)(nn * 4), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sxr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sx + m0), 0, (int)(mm * 4), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.bias ? p.bias + n0 : nullptr), 0, p.bias ? (int)(nn * 2) : 0, kRsrcWord3);
+    const bool grow = EPI == VDN_FP8_EPI_GATE && FAST;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        grow ? (void*)(p.gate + n0) : (void*)(p.gate_index ? p.gate_index + m0 : nullptr), 0,
+        grow ? (int)(nn * 2) : (p.gate_index ? (int)(mm * 4) : 0), kRsrcWord3);
+    const uint32_t l16 = (uint32_t)lane * 16, l8 = (uint32_t)lane * 8;
+    const i32x4_t vsw = __builtin_amdgcn_raw_buffer_load_b128(swr, l16, 0, 0);
+    const i32x4_t vsx = __builtin_amdgcn_raw_buffer_load_b128(sxr, l16, 0, 0);
+    const i32x2_t vb = __builtin_amdgcn_raw_buffer_load_b64(br, l8, 0, 0);
+    const i32x4_t vg4 = grow ? i32x4_t{} : __builtin_amdgcn_raw_buffer_load_b128(gr, l16, 0, 0);
+    const i32x2_t vg2 = grow ? __builtin_amdgcn_raw_buffer_load_b64(gr, l8, 0, 0) : i32x2_t{};
+    *reinterpret_cast<i32x4_t*>(scal + l16) = vsw;
+    *reinterpret_cast<i32x4_t*>(scal + 1024 + l16) = vsx;
+    *reinterpret_cast<i32x2_t*>(scal + 2048 + l8) = vb;
+    if (grow) *reinterpret_cast<i32x2_t*>(scal + 3072 + l8) = vg2;
+    else *reinterpret_cast<i32x4_t*>(scal + 3072 + l16) = vg4;
+}
+
+// Last round of a shape that runs whole tiles (no split along K), with at most a quarter of
+// the compute units busy in it: each of those 256 x 256 tiles as four 128 x 128 quadrants, one
+// workgroup of four waves per quadrant, wave w computing the quadrant's 64 x 64 part
+// (columns 64 (w & 1) .., rows 64 (w >> 1) ..) by the main kernel's MFMAs on the same
+// fragments, K blocks in the tile's rotated order -- every output the same accumulation,
+// so the same bits as the main kernel -- then the same epilogue on its two slabs: four
+// times the matrix cores on those tiles (H3 fused QKV [13107, 21504, 5376]: 4368 tiles =
+// 17 rounds + 16; small shapes of at most 64 tiles wholly).
+// K blocks double-buffered in LDS (X rows, then W rows, the main kernel's row swizzle),
+// the next block's copies issued after the barrier that frees its stage. A quadrant moves
+// 32 KiB per K block for a quarter of a tile's MFMAs, so the CU's fill rate bounds it:
+// about half a tile's time, not a quarter ([1000, 1000, 8192], 16 tiles: 0.039 against
+// 0.067 ms; four stages with the next block's fragments read under the MFMAs: 0.049 ms).
+// Used only when the quadrants fit one round (at most a quarter of the compute units
+// busy in the last round: [2000, 3000, 4096], 96 tiles as 384 quadrant workgroups, took
+// 0.045 against 0.042 ms).
+template <int EPI, bool FAST>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemm_fp8_quad(GemmArgs p)
+{
+    using namespace mainloop;
+    constexpr int QB = 128;                        // quadrant rows (X) and columns (W)
+    constexpr int kQStage = 2 * QB * BK;           // 32 KiB: X rows, then W rows
+    __shared__ __attribute__((aligned(1024))) uint8_t qs[2 * kQStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t scal[4096];
+    __shared__ __attribute__((aligned(16))) uint8_t stg[4 * kStgWave];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int quad = blockIdx.x & 3, r = blockIdx.x >> 2;
+    int tm, tn;
+    tile_coords(p.t_main + r, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t mq = m0 + QB * (quad >> 1), nq = n0 + QB * (quad & 1);
+    if (mq >= p.M || nq >= p.N) return;            // a quadrant wholly past the output
+    const int nk = (int)(p.K / BK);
+    const int phase = p.k_phase_mod > 0 ? (((tm + tn) % p.k_phase_mod) * p.k_phase_step) % nk : 0;
+    if (w == 3) stage_tile_vectors<EPI, FAST>(p, scal, m0, n0, lane);
+    // Copies: wave w fills LDS rows 32 w .. 32 w + 31 of the X rows (i < 4) and of the W
+    // rows, 8 rows (1 KiB) per copy; lane L lands at row + L/8, physical chunk L%8, so it
+    // fetches logical chunk (L%8) ^ row_swizzle(row).
+    const i32x4_t xr = rsrc_words(p.xq + mq * p.ldx, min(p.M - mq, (int64_t)QB) * p.ldx);
+    const i32x4_t wr = rsrc_words(p.wq + nq * p.ldw, min(p.N - nq, (int64_t)QB) * p.ldw);
+    uint32_t xoff[4], woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 32 * w + 8 * i + (lane >> 3);
+        const int c = (lane & 7) ^ row_swizzle(row);
+        xoff[i] = (uint32_t)(row * p.ldx) + c * 16;
+        woff[i] = (uint32_t)(row * p.ldw) + c * 16;
+    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void_t*)qs;
+    asm volatile("s_nop 4");   // SGPR write by VALU -> use as a buffer descriptor
+    auto copies = [&](int st, int kb) {
+        const uint32_t dst = lds_base + (uint32_t)st * kQStage, soff = (uint32_t)kb * BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) copy16_to_lds(xr, dst + (32 * w + 8 * i) * BK, xoff[i], soff);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) copy16_to_lds(wr, dst + (QB + 32 * w + 8 * i) * BK, woff[i], soff);
+    };
+    // fragments as the main kernel reads them: 16 rows x 128 K bytes, lane L row L % 16,
+    // bytes 32 (L / 16) .. + 31 as two 16-byte chunks
+    const int fr = lane & 15, fg = lane >> 4;
+    auto read_frag = [&](const uint8_t* s, int row) -> i32x8_t {
+        const uint4 lo = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg));
+        const uint4 hi = *reinterpret_cast<const uint4*>(s + lds_off(row, 2 * fg + 1));
+        return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+    const int th = w & 1, up = w >> 1;
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{};
+    copies(0, phase);
+    for (int j = 0; j < nk; ++j) {
+        // this wave's copies of block j have landed and its reads of block j - 1 are done;
+        // then every wave's, and block j - 1's stage is free for block j + 1
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        __syncthreads();
+        if (j + 1 < nk) {
+            const int kb = phase + j + 1;
+            copies((j + 1) & 1, kb >= nk ? kb - nk : kb);
+        }
+        const uint8_t* s = qs + (j & 1) * kQStage;
+        i32x8_t wf[4], xf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wf[i] = read_frag(s + QB * BK, 64 * th + 16 * i + fr);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xf[i] = read_frag(s, 64 * up + 16 * i + fr);
+#pragma unroll
+        for (int jx = 0; jx < 4; ++jx)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][jx] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[jx], acc[i][jx], 0, 0, 0, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __syncthreads();   // the vectors are staged
+    // the epilogue of the slabs (th, u = 2 up, 2 up + 1): accumulator (i, j) of this wave
+    // is the main kernel's (4 th + i, 4 up + j)
+    f32x4_t acc8[8][8];
+    auto run = [&](auto tc, auto uc) {
+        constexpr int TH = decltype(tc)::value, UP = decltype(uc)::value;
+        constexpr int kMask = (3 << (4 * (1 - TH) + 2 - 2 * UP));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) acc8[4 * TH + i][4 * UP + jj] = acc[i][jj];
+        tile_epilogue<EPI, FAST, kMask>(p, scal, stg + w * kStgWave, acc8, m0, n0, quad);
+    };
+    switch (w) {
+        case 0: run(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}); break;
+        case 2: run(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}); break;
+        default: run(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}); break;
+    }
+}
+
 // Split-K reduction: one workgroup of four waves per quadrant of a split tile (four per
 // tile). Wave w sums accumulators 16 w .. 16 w + 15 of the quadrant (per lane) over the
 // tile's units in slice order (slice 0 + slice 1 + ..., binary32: the order depends only
@@ -891,29 +1043,7 @@ void k_gemm_splitk_reduce(GemmArgs p)
     int tm, tn;
     tile_coords(p.t_main + r, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    // (branch-free buffer loads, all in flight at once: entries past N or M read as zeros)
-    if (w == 3) {
-        const int64_t nn = min(p.N - n0, (int64_t)256), mm = min(p.M - m0, (int64_t)256);
-        const __amdgpu_buffer_rsrc_t swr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sw + n0), 0, (int)(nn * 4), kRsrcWord3);
-        const __amdgpu_buffer_rsrc_t sxr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.sx + m0), 0, (int)(mm * 4), kRsrcWord3);
-        const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.bias ? p.bias + n0 : nullptr), 0, p.bias ? (int)(nn * 2) : 0, kRsrcWord3);
-        const bool grow = EPI == VDN_FP8_EPI_GATE && FAST;
-        const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
-            grow ? (void*)(p.gate + n0) : (void*)(p.gate_index ? p.gate_index + m0 : nullptr), 0,
-            grow ? (int)(nn * 2) : (p.gate_index ? (int)(mm * 4) : 0), kRsrcWord3);
-        const uint32_t l16 = (uint32_t)lane * 16, l8 = (uint32_t)lane * 8;
-        const i32x4_t vsw = __builtin_amdgcn_raw_buffer_load_b128(swr, l16, 0, 0);
-        const i32x4_t vsx = __builtin_amdgcn_raw_buffer_load_b128(sxr, l16, 0, 0);
-        const i32x2_t vb = __builtin_amdgcn_raw_buffer_load_b64(br, l8, 0, 0);
-        const i32x4_t vg4 = grow ? i32x4_t{} : __builtin_amdgcn_raw_buffer_load_b128(gr, l16, 0, 0);
-        const i32x2_t vg2 = grow ? __builtin_amdgcn_raw_buffer_load_b64(gr, l8, 0, 0) : i32x2_t{};
-        *reinterpret_cast<i32x4_t*>(scal + l16) = vsw;
-        *reinterpret_cast<i32x4_t*>(scal + 1024 + l16) = vsx;
-        *reinterpret_cast<i32x2_t*>(scal + 2048 + l8) = vb;
-        if (grow) *reinterpret_cast<i32x2_t*>(scal + 3072 + l8) = vg2;
-        else *reinterpret_cast<i32x4_t*>(scal + 3072 + l16) = vg4;
-    }
+    if (w == 3) stage_tile_vectors<EPI, FAST>(p, scal, m0, n0, lane);
     const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(p.ws + (int64_t)r * p.splits * kUnitFloatsDev + (int64_t)quad * 16384), 0,
         (int)min((int64_t)p.splits * kUnitFloatsDev * 4, (int64_t)0x7fffffff), kRsrcWord3);
@@ -952,10 +1082,10 @@ void k_gemm_splitk_reduce(GemmArgs p)
         for (int j = 0; j < 8; ++j) acc[i][j] = sums[(8 * i + j) * 64 + lane];
     uint8_t* const ws = stg + w * kStgWave;
     switch (w) {
-        case 0: tile_epilogue<EPI, FAST, 0>(p, scal, ws, acc, m0, n0, quad); break;
-        case 1: tile_epilogue<EPI, FAST, 1>(p, scal, ws, acc, m0, n0, quad); break;
-        case 2: tile_epilogue<EPI, FAST, 2>(p, scal, ws, acc, m0, n0, quad); break;
-        default: tile_epilogue<EPI, FAST, 3>(p, scal, ws, acc, m0, n0, quad); break;
+        case 0: tile_epilogue<EPI, FAST, 0x88>(p, scal, ws, acc, m0, n0, quad); break;
+        case 1: tile_epilogue<EPI, FAST, 0x44>(p, scal, ws, acc, m0, n0, quad); break;
+        case 2: tile_epilogue<EPI, FAST, 0x22>(p, scal, ws, acc, m0, n0, quad); break;
+        default: tile_epilogue<EPI, FAST, 0x11>(p, scal, ws, acc, m0, n0, quad); break;
     }
 }
 
@@ -1186,11 +1316,19 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
                 p.ws = ws;
             }
         }
+        if (!p.units) {
+            // a last round of at most a quarter of the compute units as quadrants
+            const int64_t R = T % cus;
+            if (R > 0 && 4 * R <= cus) p.t_main = (int)(T - R);   // tiles t_main .. T - 1: k_gemm_fp8_quad
+        }
         blocks = std::min<int64_t>((int64_t)p.t_main, cus);
     }
     const dim3 grid((unsigned)std::max<int64_t>(blocks, 1)), block(kThreads);
     const dim3 ugrid((unsigned)std::max(p.units, 1)), rgrid((unsigned)(p.units ? 4 * (p.units / p.splits) : 1));
     const dim3 rblock(256);
+    // (no split: the tiles past t_main run as quadrants)
+    const int quads = p.units ? 0 : (int)(T - p.t_main);
+    const dim3 qgrid((unsigned)std::max(4 * quads, 1));
     // the fast epilogue: 16-byte output rows, row offsets within 31 bits, and no
     // per-row gate or residual (a gate table of one row is staged like the bias)
     const bool gate_broadcast = epilogue == VDN_FP8_EPI_GATE && !residual && (gate_rows == 1 || !gate_index) &&
@@ -1208,6 +1346,7 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
     if (row_gate && (!residual || (int64_t)BM * ldres * 2 <= (int64_t)0x7fffffff) &&
         gate_rows * ldgate * 2 <= (int64_t)0x7fffffff) {
         if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<kEpiRowGate, true, false>), grid, block, 0, stream, p);
+        if (quads) hipLaunchKernelGGL((k_gemm_fp8_quad<kEpiRowGate, true>), qgrid, block, 0, stream, p);
         if (p.units) {
             hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
             hipLaunchKernelGGL((k_gemm_splitk_reduce<kEpiRowGate, true>), rgrid, rblock, 0, stream, p);
@@ -1216,6 +1355,7 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
     }
     if (row_gate) {
         if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, false>), grid, block, 0, stream, p);
+        if (quads) hipLaunchKernelGGL((k_gemm_fp8_quad<VDN_FP8_EPI_NONE, true>), qgrid, block, 0, stream, p);
         if (p.units) {
             hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
             hipLaunchKernelGGL((k_gemm_splitk_reduce<VDN_FP8_EPI_NONE, true>), rgrid, rblock, 0, stream, p);
@@ -1229,12 +1369,14 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
     do {                                                                                                 \
         if (main && fast) {                                                                              \
             if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<E, true, false>), grid, block, 0, stream, p);   \
+            if (quads) hipLaunchKernelGGL((k_gemm_fp8_quad<E, true>), qgrid, block, 0, stream, p);     \
             if (p.units) {                                                                               \
                 hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p); \
                 hipLaunchKernelGGL((k_gemm_splitk_reduce<E, true>), rgrid, rblock, 0, stream, p);        \
             }                                                                                            \
         } else if (main) {                                                                               \
             if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<E, false, false>), grid, block, 0, stream, p);  \
+            if (quads) hipLaunchKernelGGL((k_gemm_fp8_quad<E, false>), qgrid, block, 0, stream, p);    \
             if (p.units) {                                                                               \
                 hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p); \
                 hipLaunchKernelGGL((k_gemm_splitk_reduce<E, false>), rgrid, rblock, 0, stream, p);       \
@@ -1247,6 +1389,7 @@ int gemm_launch(const void* xq, const float* x_scale, const void* wq, const floa
         // (the general epilogue only: the fast one stages bf16 rows)
         if (main) {
             if (p.t_main) hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_F32, false, false>), grid, block, 0, stream, p);
+            if (quads) hipLaunchKernelGGL((k_gemm_fp8_quad<VDN_FP8_EPI_F32, false>), qgrid, block, 0, stream, p);
             if (p.units) {
                 hipLaunchKernelGGL((k_gemm_fp8<VDN_FP8_EPI_NONE, true, true>), ugrid, block, 0, stream, p);
                 hipLaunchKernelGGL((k_gemm_splitk_reduce<VDN_FP8_EPI_F32, false>), rgrid, rblock, 0, stream, p);
