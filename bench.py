@@ -337,7 +337,7 @@ def cpu_baseline(draws):
         affinity = None
     return {"value": round(value, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "host_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
-            "threads_note": "threads = min(16, os.cpu_count()): the GPU box's CPU share is 16 per GPU",
+            "threads_note": "threads = min(16, os.cpu_count()): the host's CPU share is 16 per GPU",
             "sample": "the whole QKV step (quantize X [32760, 5120], dequantized fp32 matmul against W "
                       "[15360, 5120] + bias) once at full size; cfg1 median of 3 after a warm-up; the other "
                       "configs' kernel-equivalents once each at full size (oracle C quantizers and merge, numpy "

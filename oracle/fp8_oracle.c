@@ -1,6 +1,7 @@
 /*
  * fp8_oracle.c -- CPU restatement of the reference's fp8 quantized-linear
- * arithmetic, used ONLY as test infrastructure (the checker): tests/, the
+ * arithmetic, used ONLY as test infrastructure (what results are compared
+ * with): tests/, the
  * smoke check in __graft_entry__.py and the cpu_baseline leg of bench.py load
  * it. Nothing in the product path links, loads or calls this file.
  *

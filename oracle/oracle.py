@@ -1,7 +1,7 @@
 """CPU oracle for the fp8 quantized-linear path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, `__graft_entry__.smoke()` and the `cpu_baseline` leg of bench.py may
-import this module, and only as the checker. The product (the `vdn_fp8` package and
+import this module, and only to compare the product's results with it. The product (the `vdn_fp8` package and
 its HIP library) never imports it and has no CPU fallback.
 
 Bit-level arithmetic (e4m3 / bf16 rounding, the row and weight quantizers, the LoRA

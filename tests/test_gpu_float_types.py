@@ -6,7 +6,7 @@ weight's own type, :262-267; `forward` passes out_dtype=rows.dtype, :279-283).
 
 Codes and scales are compared bit for bit with the oracle (any two NaN codes count as
 equal); SwiGLU codes within one step (sigmoid is transcendental); the GEMM's output within
-the north star's max-abs 2e-2 and rel-L2 1e-3 of the oracle's float64 product rounded to
+the parity bounds (max-abs 2e-2, rel-L2 1e-3) of the oracle's float64 product rounded to
 the output type, and against the reference's own torch._scaled_mm call with the same
 out_dtype on the same codes."""
 import numpy as np
@@ -95,7 +95,7 @@ def _linear(N, K, dtype, device, seed, bias=True):
 def test_fp8_linear_float_model(device, dtype, M, N, K):
     """Fp8Linear on a float16 / float32 Linear, fed rows of that type: the weight codes
     bit-exact with the oracle, the activation codes too, the output (of the rows' type)
-    within the north star's bounds of the oracle and of the reference's own
+    within the parity bounds of the oracle and of the reference's own
     torch._scaled_mm(out_dtype=that type) + bias on the same codes. K = 400 takes the
     kernel for K not a multiple of 256."""
     print(f"Fp8Linear {dtype} [{M}, {N}, {K}]", flush=True)
