@@ -526,6 +526,8 @@ def main():
                                           "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         # one DiT block's four linears on the LoRA workload's own input (seed 5): the QKV
         # weight with its LoRA merged, attention-out + gate, FFN-up + GELU, FFN-down + gate
+        # (the GELU applied by the FFN-down input's quantizer, gelu_quantize: the same codes
+        # as the FFN-up GEMM's GELU epilogue followed by quantize_rows)
         qkv = _make_linear(blk["w0"], blk["qkv_bias"], dev, lora=(ad, bd, lscale))
         out_l = _make_linear(blk["w_out"], None, dev)
         up_l = _make_linear(blk["w_up"], blk["b_up"], dev)
@@ -539,8 +541,8 @@ def main():
             qx, sx = vdn_fp8.quantize_rows(x5)
             out_l.forward_quantized(qx, sx, epilogue="gate", gate=gate_d)
             qx, sx = vdn_fp8.quantize_rows(x5)
-            hh = up_l.forward_quantized(qx, sx, epilogue="gelu_tanh")
-            qh, sh = vdn_fp8.quantize_rows(hh)
+            hh = up_l.forward_quantized(qx, sx)
+            qh, sh = vdn_fp8.gelu_quantize(hh)
             dn_l.forward_quantized(qh, sh, epilogue="gate", gate=gate_d)
 
         block()

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VDN_FP8_ABI_VERSION 4
+#define VDN_FP8_ABI_VERSION 5
 
 /* status codes */
 #define VDN_FP8_OK 0
@@ -67,6 +67,22 @@ extern "C" {
  */
 int vdn_fp8_quantize_rows(const void *x, int64_t M, int64_t K, int64_t ldx,
                           void *y, int64_t ldy, float *scale, hipStream_t stream);
+
+/*
+ * Fused GELU(tanh) + per-token quantization of h (bf16 [M, K], the FFN-up
+ * projection's bf16 output before its activation): each element replaced by
+ * bf16(gelu_tanh(h)) -- the same function, on the same bf16 value, as the GEMM's
+ * VDN_FP8_EPI_GELU_TANH epilogue, so the codes are bit for bit those of that
+ * epilogue's output passed to vdn_fp8_quantize_rows -- then the quantize_rows
+ * arithmetic on those values (y e4m3 [M, K], scale [M]).
+ * Replaces: quantize_rows (src/models/ops/fp8_linear.py:110-117) of a GELU(tanh) FFN's
+ *           down-projection input, with the activation folded in (the reference's FFN is
+ *           SwiGLU; a GELU FFN is the benchmark DiT block's).
+ * Requires: K % 8 == 0, K <= 16384, ldh % 8 == 0, ldy % 8 == 0, h 16-byte and y 8-byte
+ *           aligned.
+ */
+int vdn_fp8_gelu_quantize_rows(const void *h, int64_t M, int64_t K, int64_t ldh,
+                               void *y, int64_t ldy, float *scale, hipStream_t stream);
 
 /*
  * Fused SwiGLU + per-token quantization of h (bf16 [M, 2K], value half first,

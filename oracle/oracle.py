@@ -24,6 +24,8 @@ Reference functions restated (paths relative to the reference checkout):
   gelu_tanh             no reference function (the reference FFN is SwiGLU); the textbook
                         tanh approximation of GELU, pinned against torch's
                         F.gelu(approximate="tanh")
+  gelu_quantize_rows    quantize_rows (fp8_linear.py:110-117) of bf16(gelu_tanh(h)): a GELU
+                        FFN's down-projection input
   gated / gated_residual  src/models/ops/fused_block.py:47-49 (_post_ref, as the compiled
                         `post` evaluates it: one bf16 rounding)
   norm_quantize_rows    src/models/ops/fused_block.py:41-44 (_pre_ref, as the compiled
@@ -241,6 +243,15 @@ def _bf16_round(v):
     """Round float64 values to bf16 (through binary32, as torch's .to(bfloat16) of a
     float32 tensor does) and return them as float64."""
     return bf16_decode(bf16_encode(np.asarray(v, np.float64).astype(np.float32))).astype(np.float64)
+
+
+def gelu_quantize_rows(h):
+    """bf16 bits [M, K] -> (e4m3 codes [M, K], fp32 scale [M]): each element replaced by
+    bf16(gelu_tanh(h)) (the textbook formula in float64, rounded through binary32 as a
+    bf16 cast of a float32 result rounds), then quantize_rows."""
+    h = _u16(h)
+    g = gelu_tanh(bf16_decode(h).astype(np.float64))
+    return quantize_rows(bf16_encode(g.astype(np.float32)))
 
 
 def dequant_linear_typed(qx, sx, qw, sw, bias=None, out_dtype=np.float32):

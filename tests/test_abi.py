@@ -19,7 +19,8 @@ def declared_symbols():
 
 def test_header_declares_the_abi():
     names = declared_symbols()
-    assert {"vdn_fp8_quantize_rows", "vdn_fp8_swiglu_quantize_rows", "vdn_fp8_requantize_weight",
+    assert {"vdn_fp8_quantize_rows", "vdn_fp8_swiglu_quantize_rows", "vdn_fp8_gelu_quantize_rows",
+            "vdn_fp8_requantize_weight",
             "vdn_fp8_gemm", "vdn_fp8_norm_quantize_rows", "vdn_fp8_qk_prep", "vdn_fp8_gated_residual",
             "vdn_fp8_last_error",
             "vdn_fp8_abi_version"} <= set(names)
@@ -97,6 +98,12 @@ FAKE = 1 << 20        # never dereferenced: every call below fails validation fi
     (lambda l: l.vdn_fp8_quantize_rows_typed(FAKE, 2, -1, 8, 8, FAKE, 8, FAKE, None), "negative"),
     (lambda l: l.vdn_fp8_swiglu_quantize_rows_typed(FAKE, 2, 4, 8, 8, FAKE, 8, FAKE, None), "ldx >= 16"),
     (lambda l: l.vdn_fp8_requantize_weight_typed(None, 1, 4, 8, 8, FAKE, 8, FAKE, None), "null"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(FAKE, 4, 16392, 16392, FAKE, 16392, FAKE, None), "16384"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(FAKE, 4, 12, 12, FAKE, 12, FAKE, None), "multiples of 8"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(FAKE, 4, 16, 8, FAKE, 16, FAKE, None), "ldh, ldy >= K"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(FAKE + 8, 4, 8, 8, FAKE, 8, FAKE, None), "aligned"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(None, 4, 8, 8, FAKE, 8, FAKE, None), "null"),
+    (lambda l: l.vdn_fp8_gelu_quantize_rows(FAKE, -1, 8, 8, FAKE, 8, FAKE, None), "negative"),
     (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, FAKE, 3, None, None, 0, 0, None, 0, FAKE, 4, None), "binary32"),
     (lambda l: l.vdn_fp8_gemm(FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 32, 32, None, 3, None, None, 0, 0, None, 0, FAKE + 8, 4, None), "binary32"),
 ])
@@ -111,6 +118,7 @@ def test_empty_problems_are_no_ops():
     import vdn_fp8._lib as L
     lib = L.load()
     assert lib.vdn_fp8_quantize_rows(None, 0, 8, 8, None, 8, None, None) == L.OK
+    assert lib.vdn_fp8_gelu_quantize_rows(None, 0, 8, 8, None, 8, None, None) == L.OK
     assert lib.vdn_fp8_gemm(None, None, None, None, 0, 16, 32, 32, 32, None, 0, None, None, 0, 0, None, 0, None, 16, None) == L.OK
     assert lib.vdn_fp8_requantize_weight(None, 0, 8, 8, None, None, 0, 1.0, None, 8, None, None, None) == L.OK
     assert lib.vdn_fp8_norm_quantize_rows(None, 0, 8, 8, None, 1e-6, None, None, 0, None, 0, None, 8, None,

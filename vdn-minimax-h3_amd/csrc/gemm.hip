@@ -119,17 +119,6 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& p, int nk, int v, int&
     }
 }
 
-// gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3):
-// exp(-2u) = 2^t with t = v (A + B v^2), A = -2 sqrt(2/pi) log2(e), B = 0.044715 A
-// (the constants folded so that t costs three operations and exp one).
-__device__ __forceinline__ float gelu_tanh(float v)
-{
-    constexpr float kA = -2.3022082f;            // -1.5957691216057308 * 1.4426950408889634
-    constexpr float kB = -0.10294324f;           // kA * 0.044715
-    const float t = v * __builtin_fmaf(kB, v * v, kA);
-    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
-}
-
 // Renumbers workgroup b so that XCD (b % 8) gets a contiguous run of tiles,
 // then maps the run index to (tile_m, tile_n) in groups of gm m-tiles.
 __device__ __forceinline__ void tile_coords(int b, int tiles_m, int tiles_n, int gm, int& tm, int& tn)

@@ -95,7 +95,10 @@ __device__ __forceinline__ uint2 quantize_chunk(uint4 v, float s, float r)
 // LDS. More waves per row cut the registers per wave and multiply the
 // workgroups: [32760, 5120] activations in 0.075 ms with two against 0.077 ms with
 // one (non-temporal loads in both), 76.3 against 77.3 us with four against two.
-template <int CPL, bool kWeight, int WPR, bool NT>
+// GELU: the row is first replaced by bf16(gelu_tanh(x)) of each element (the GEMM
+// epilogue's GELU of its bf16 output, so the codes are those of that epilogue's output
+// quantized by this kernel).
+template <int CPL, bool kWeight, int WPR, bool NT, bool GELU = false>
 __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
     uint8_t* __restrict__ y, int64_t ldy, float* __restrict__ scale_out)
@@ -116,6 +119,15 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_rowquant(
     for (int c = 0; c < CPL; ++c) {
         const int idx = part * kLanes + lane + kLanes * WPR * c;
         v[c] = (valid && idx < nch) ? load_once(xr + idx) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if constexpr (GELU) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w4[e] = pack_bf16x2(gelu_tanh(bf16_lo(w4[e])), gelu_tanh(bf16_hi(w4[e])));
+            v[c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
     }
     uint32_t m2 = 0;
 #pragma unroll
@@ -920,7 +932,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kLanes) void k_swiglu_quant_split(
 // an instantiated CPL; [32760, 13824]: 0.224 ms against 0.229 ms with two; [32760,
 // 5120] 76.3 against 77.3 us, the [15360, 5120] weight 39.4 against 39.9 us).
 // Returns false for other widths.
-template <bool kWeight, bool NT>
+template <bool kWeight, bool NT, bool GELU = false>
 bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
                           uint8_t* y, int64_t ldy, float* s)
 {
@@ -931,7 +943,7 @@ bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t 
     const dim3 grid((unsigned)M);
 #define VDN_CASE(n)                                                                                    \
     if (per <= n) {                                                                                    \
-        hipLaunchKernelGGL((k_rowquant<n, kWeight, 4, NT>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        hipLaunchKernelGGL((k_rowquant<n, kWeight, 4, NT, GELU>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
         return true;                                                                                   \
     }
     VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(5) VDN_CASE(6) VDN_CASE(7) VDN_CASE(8)
@@ -939,7 +951,7 @@ bool launch_rowquant_pair(hipStream_t st, const uint16_t* x, int64_t M, int64_t 
     return false;
 }
 
-template <bool kWeight>
+template <bool kWeight, bool GELU = false>
 void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t K,
                      int64_t ldx, uint8_t* y, int64_t ldy, float* s)
 {
@@ -947,19 +959,20 @@ void launch_rowquant(int cpl, dim3 grid, hipStream_t st, const uint16_t* x, int6
     // every weight (its codes are read by later GEMMs, not by the next kernel: [15360,
     // 5120] 37.7 us against 38.3 us cached, weight read from HBM)
     const bool nt = kWeight || M * K >= kNtStoreBytes;
-    if (nt ? launch_rowquant_pair<kWeight, true>(st, x, M, K, ldx, y, ldy, s)
-           : launch_rowquant_pair<kWeight, false>(st, x, M, K, ldx, y, ldy, s))
+    if (nt ? launch_rowquant_pair<kWeight, true, GELU>(st, x, M, K, ldx, y, ldy, s)
+           : launch_rowquant_pair<kWeight, false, GELU>(st, x, M, K, ldx, y, ldy, s))
         return;
     const dim3 block(kWavesPerBlock * kLanes);
 #define VDN_CASE(n)                                                                           \
     case n:                                                                                   \
-        if (nt) hipLaunchKernelGGL((k_rowquant<n, kWeight, 1, true>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
-        else hipLaunchKernelGGL((k_rowquant<n, kWeight, 1, false>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        if (nt) hipLaunchKernelGGL((k_rowquant<n, kWeight, 1, true, GELU>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
+        else hipLaunchKernelGGL((k_rowquant<n, kWeight, 1, false, GELU>), grid, block, 0, st, x, M, K, ldx, y, ldy, s); \
         return;
     switch (cpl) {
         VDN_CASE(1) VDN_CASE(2) VDN_CASE(3) VDN_CASE(4) VDN_CASE(6) VDN_CASE(8) VDN_CASE(10)
         VDN_CASE(12) VDN_CASE(16) VDN_CASE(20) VDN_CASE(24) VDN_CASE(28) VDN_CASE(32)
-        default: hipLaunchKernelGGL((k_rowquant_wide<kWeight>), grid, block, 0, st, x, M, K, ldx, y, ldy, s);
+        default:   // (the GELU entry point takes rows of at most 16384 elements)
+            if constexpr (!GELU) hipLaunchKernelGGL((k_rowquant_wide<kWeight>), grid, block, 0, st, x, M, K, ldx, y, ldy, s);
     }
 #undef VDN_CASE
 }
@@ -989,6 +1002,26 @@ extern "C" int vdn_fp8_quantize_rows(const void* x, int64_t M, int64_t K, int64_
     const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
     launch_rowquant<false>(pick_cpl(K / 8), grid, stream, (const uint16_t*)x, M, K, ldx, (uint8_t*)y, ldy, scale);
     return check_launch("quantize_rows");
+}
+
+extern "C" int vdn_fp8_gelu_quantize_rows(const void* h, int64_t M, int64_t K, int64_t ldh, void* y,
+                                          int64_t ldy, float* scale, hipStream_t stream)
+{
+    if (M < 0 || K < 0) return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: negative shape [%lld, %lld]", (long long)M, (long long)K);
+    if (M == 0 || K == 0) {
+        if (M > 0 && K == 0) return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: K must be positive");
+        return VDN_FP8_OK;
+    }
+    if (!h || !y || !scale) return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: null pointer");
+    if (K % 8 || ldh % 8 || ldy % 8 || ldh < K || ldy < K)
+        return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: need K, ldh, ldy multiples of 8 and ldh, ldy >= K (K=%lld ldh=%lld ldy=%lld)",
+                         (long long)K, (long long)ldh, (long long)ldy);
+    if (!aligned(h, 16) || !aligned(y, 8) || !aligned(scale, 4))
+        return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: h must be 16-byte and y 8-byte aligned");
+    if (K / 8 > 32 * kLanes) return set_error(VDN_FP8_EINVAL, "gelu_quantize_rows: K=%lld above the supported 16384", (long long)K);
+    const dim3 grid((unsigned)((M + kWavesPerBlock - 1) / kWavesPerBlock));
+    launch_rowquant<false, true>(pick_cpl(K / 8), grid, stream, (const uint16_t*)h, M, K, ldh, (uint8_t*)y, ldy, scale);
+    return check_launch("gelu_quantize_rows");
 }
 
 extern "C" int vdn_fp8_swiglu_quantize_rows(const void* h, int64_t M, int64_t K, int64_t ldh, void* y,

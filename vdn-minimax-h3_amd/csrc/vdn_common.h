@@ -61,6 +61,18 @@ __device__ __forceinline__ float round_bf16_hi(float v)
     return __builtin_bit_cast(float, d);
 }
 
+// GELU(tanh), shared by the GEMM epilogue and the GELU quantizer so that both give the
+// same bits: gelu_tanh(v) = 0.5 v (1 + tanh(u)) = v * sigmoid(2u), u = sqrt(2/pi) (v + 0.044715 v^3):
+// exp(-2u) = 2^t with t = v (A + B v^2), A = -2 sqrt(2/pi) log2(e), B = 0.044715 A
+// (the constants folded so that t costs three operations and exp one).
+__device__ __forceinline__ float gelu_tanh(float v)
+{
+    constexpr float kA = -2.3022082f;            // -1.5957691216057308 * 1.4426950408889634
+    constexpr float kB = -0.10294324f;           // kA * 0.044715
+    const float t = v * __builtin_fmaf(kB, v * v, kA);
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
 // 16-byte load of data read exactly once (activations streamed through a
 // kernel): non-temporal, so the stream does not displace cached lines that are
 // read again (the activation quantizer on [32760, 5120]: 0.080 ms against

@@ -8,7 +8,7 @@ block's pre-norm (`src.models.ops.fused_block`) with the quantization that follo
 (hand-written HIP for gfx950, C ABI in include/vdn_fp8.h).
 """
 from .fp8_linear import (FP8_DTYPE, MIN_WIDTH, SKIP_END_BLOCKS, _FP8_MAX, Fp8Linear,
-                         convert_linear_to_fp8, per_tensor_gemm, quantize_activation,
+                         convert_linear_to_fp8, gelu_quantize, per_tensor_gemm, quantize_activation,
                          quantize_rows, quantize_rows_reference, requantize_weight,
                          set_index_checks, swiglu_quantize, swiglu_quantize_activation)
 from .fused_block import fast_block_forward, fast_ff_forward, post, pre, pre_quantize
@@ -16,7 +16,7 @@ from .lora import load_external_lora, merge_lora_and_convert, merge_lora_state
 from .softmax_attention import qk_prep
 
 __all__ = [
-    "FP8_DTYPE", "MIN_WIDTH", "SKIP_END_BLOCKS", "_FP8_MAX", "Fp8Linear", "convert_linear_to_fp8",
+    "FP8_DTYPE", "MIN_WIDTH", "SKIP_END_BLOCKS", "_FP8_MAX", "Fp8Linear", "convert_linear_to_fp8", "gelu_quantize",
     "per_tensor_gemm", "quantize_activation", "quantize_rows", "quantize_rows_reference",
     "requantize_weight", "swiglu_quantize", "swiglu_quantize_activation", "load_external_lora",
     "merge_lora_and_convert", "merge_lora_state", "pre_quantize", "qk_prep", "pre", "post",

@@ -12,7 +12,7 @@ import os
 
 from .build import CSRC, INCLUDE, LIB_PATH, compiler_id, source_manifest
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, EINVAL, ELAUNCH = 0, 1, 2
 EPI_NONE, EPI_GELU_TANH, EPI_GATE, EPI_F32 = 0, 1, 2, 3
@@ -25,6 +25,7 @@ _build_info = None
 _P, _I64, _F32, _I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
 EXPORTS = (
     ("vdn_fp8_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    ("vdn_fp8_gelu_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     ("vdn_fp8_swiglu_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     ("vdn_fp8_norm_quantize_rows", _I32, [_P, _I64, _I64, _I64, _P, _F32, _P, _P, _I64, _P, _I64, _P, _I64, _P,
                                           _P, _I64, _P]),

@@ -167,6 +167,25 @@ def swiglu_quantize(h):
     return y, scale
 
 
+def gelu_quantize(h):
+    """GELU(tanh) and per-token quantization in one kernel. h is a GELU FFN's up-projection
+    output before its activation, bf16 [M, K] (K <= 16384): each element becomes
+    bf16(gelu_tanh(h)) -- the GEMM's "gelu_tanh" epilogue on the same bf16 value, so the
+    codes are bit for bit quantize_rows(forward_quantized(..., epilogue="gelu_tanh")) --
+    and the rows are quantized as in `quantize_rows`; returns e4m3 [M, K] and scales
+    [M, 1]. The activation costs less here, where the row quantizer is bound by HBM, than
+    in the GEMM's epilogue, where the matrix cores wait for it. The reference's FFN is
+    SwiGLU (see `swiglu_quantize`); this serves a GELU FFN's down projection, whose
+    quantize_rows it replaces (fp8_linear.py:110-117)."""
+    h = _rows(h)
+    M, K = h.shape
+    y = torch.empty(M, K, device=h.device, dtype=FP8_DTYPE)
+    scale = torch.empty(M, 1, device=h.device, dtype=torch.float32)
+    _lib.check(_lib.load().vdn_fp8_gelu_quantize_rows(_ptr(h), M, K, h.stride(0), _ptr(y), K, _ptr(scale), _stream(h)),
+               "gelu_quantize")
+    return y, scale
+
+
 def quantize_rows_reference(x):
     """The eager spelling of `quantize_rows` (fp8_linear.py:132-135), kept for API
     compatibility: plain torch ops, the contract the HIP kernel is bit-exact with.
