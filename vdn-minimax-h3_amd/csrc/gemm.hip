@@ -40,6 +40,13 @@
 //
 // K % 128 != 0 goes to a second kernel (BK = 128, 16x16x128 MFMA, two stages)
 // whose last step is filled through VGPRs with zeros past K.
+//
+// The last round of tiles, when it would leave most compute units idle: rows of
+// K >= 8192 split it along K (units storing binary32 partial sums to a
+// workspace, then k_gemm_splitk_reduce); other shapes with at most a quarter of
+// the units busy run it as 128 x 128 quadrants (k_gemm_fp8_quad, the same bits
+// as whole tiles). A per-row gate and the residual apply in the fast epilogue's
+// row layout (kEpiRowGate).
 #include <stdint.h>
 
 #include <algorithm>
