@@ -570,6 +570,11 @@ def main():
         gbs = wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9
         extra["quantize_rows_13824"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
                                         "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
+        # the same rows through GELU(tanh) first (the DiT block's FFN-down input)
+        ms = _time_region(lambda: vdn_fp8.gelu_quantize(x4d_dev), reps)
+        gbs = wl.quant_bytes(M, 13824) / (ms * 1e-3) / 1e9
+        extra["gelu_quantize_13824"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / PEAK_HBM_GBPS, 4)}
         del q3, q4d, q4o, up3, dn4, out4, x4d_dev
         # The QKV GEMM again with every code of X and W set to e4m3 1.0: same instructions, same
         # memory traffic, but operands that toggle no multiplier bits. The gap to the line above
@@ -729,7 +734,7 @@ def main():
             ("quantize_rows", "pre_norm_quantize"): (2 * M * K, M * K + 4 * M, False, 1),
             ("pre_norm_quantize_h3",): (2 * 13107 * 5376, 13107 * 5376 + 4 * 13107, False, 1),
             ("requantize_weight", "lora_merge_requantize"): (2 * nw_ * kw_, nw_ * kw_ + 4 * nw_, False, 3),
-            ("quantize_rows_13824",): (2 * M * 13824, M * 13824 + 4 * M, M * 13824 >= (256 << 20), 1),
+            ("quantize_rows_13824", "gelu_quantize_13824"): (2 * M * 13824, M * 13824 + 4 * M, M * 13824 >= (256 << 20), 1),
             ("swiglu_quantize_h3",): (4 * M * 14336, M * 14336 + 4 * M, True, 1),
             ("post_gated_residual",): (2 * M * K * 2, M * K * 2, True, 1),
             ("qk_prep_q",): (M * 5120 * 2, M * 5120 * 2, True, 1),
