@@ -198,15 +198,6 @@ __device__ __forceinline__ const uint16_t* gate_row(const GemmArgs& p, int64_t m
 // of a tile: rows past M (or N) read as zeros. Wave-uniform, so in SGPRs.
 constexpr int kRsrcWord3 = 0x00020000;
 
-__device__ __forceinline__ i32x4_t tile_rsrc_words(const uint8_t* base, int64_t rows, int64_t ld)
-{
-    const uint64_t a = (uint64_t)base;
-    const int64_t bytes = min(min(rows, (int64_t)256) * ld, (int64_t)0x7fffffff);
-    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(a & 0xffffffffu)),
-                   __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
-                   __builtin_amdgcn_readfirstlane((int)bytes), kRsrcWord3};
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint8_t* base, int64_t rows, int64_t ld)
 {
     const int64_t bytes = min(rows, (int64_t)256) * ld;
@@ -276,7 +267,6 @@ constexpr int BK = 128;                     // K bytes per block (one LDS stage)
 constexpr int kStage = (BM + BN) * BK;      // 64 KiB: X tile, then W tile
 constexpr int kCopies = BM * BK / 1024 / 4; // 1 KiB copies per wave per tile per block (8)
 constexpr int kBlockCopies = 2 * kCopies;   // X and W: 16 per wave per block
-constexpr int kNoVmWait = 63;               // s_waitcnt vmcnt field maximum: no condition
 constexpr int kScal = 2 * kStage;           // per-tile vectors, two buffers of 4 x 1 KiB
 constexpr int kStgRow = 144;                // epilogue staging row: 128 bytes + 16 of padding
 constexpr int kStgWave = 32 * kStgRow;      // 32 rows per wave

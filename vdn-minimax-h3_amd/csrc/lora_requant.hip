@@ -747,7 +747,7 @@ __global__ __launch_bounds__(rows::kThreads) void k_lora_rows(RowArgs p)
                     lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
             }
         };
-        auto mfmas = [&](int c, const bf16x8_t (&aop)[kSteps]) {
+        auto mfmas = [&](int, const bf16x8_t (&aop)[kSteps]) {
             f32x16_t a = f32x16_t{};
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[s], bop[s], a, 0, 0, 0);
